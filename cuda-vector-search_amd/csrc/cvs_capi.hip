@@ -1,0 +1,507 @@
+// C-ABI of libcvs_hip.so: planning, validation and launch sequencing.
+//
+// Replaces the pybind11 host half of csrc/kernels.cu:451-592 (check_matrix,
+// check_pair, scores, slots_per_lane, fused_topk, PYBIND11_MODULE).  Every entry
+// point takes raw device pointers, sizes, a device index and a hipStream_t, and
+// allocates nothing: the caller owns outputs and the workspace (sized by
+// cvs_fused_plan).  Launches are asynchronous on the given stream; nothing here
+// synchronises.  Errors are reported as a non-zero status plus a thread-local
+// message (cvs_last_error), mirroring the reference's TORCH_CHECK messages.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "cvs.h"
+#include "cvs_kernels.h"
+
+using namespace cvs;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(CVS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DevInfo {
+  bool ready = false;
+  bool gfx950 = false;
+  int cus = 0;
+  char arch[64] = {0};
+};
+
+constexpr int kMaxDevices = 64;
+DevInfo g_dev[kMaxDevices];
+std::mutex g_dev_mu;
+
+int dev_info(int device, DevInfo* out) {
+  if (device < 0 || device >= kMaxDevices) return fail(CVS_ERR_INVALID, "invalid device index %d", device);
+  std::lock_guard<std::mutex> lock(g_dev_mu);
+  DevInfo& di = g_dev[device];
+  if (!di.ready) {
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    di.cus = prop.multiProcessorCount;
+    std::snprintf(di.arch, sizeof di.arch, "%s", prop.gcnArchName);
+    di.gfx950 = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    di.ready = true;
+  }
+  *out = di;
+  return CVS_OK;
+}
+
+// Switches to `device` for the lifetime of the guard (the reference's CUDAGuard).
+struct DeviceGuard {
+  int prev = -1;
+  bool switched = false;
+  hipError_t err = hipSuccess;
+  explicit DeviceGuard(int device) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != device) {
+      err = hipSetDevice(device);
+      switched = (err == hipSuccess);
+    }
+  }
+  ~DeviceGuard() {
+    if (switched) (void)hipSetDevice(prev);
+  }
+};
+
+int check_inputs(const void* q, const void* x, int64_t nq, int64_t n, int64_t d) {
+  if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
+  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (n < 0 || n >= INT_MAX) return fail(CVS_ERR_INVALID, "corpus must have fewer than 2^31 rows");
+  if (nq < 0 || nq >= INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
+  if (nq > 0 && (q == nullptr || reinterpret_cast<uintptr_t>(q) % 16 != 0))
+    return fail(CVS_ERR_INVALID, "queries must be 16-byte aligned");
+  if (n > 0 && (x == nullptr || reinterpret_cast<uintptr_t>(x) % 16 != 0))
+    return fail(CVS_ERR_INVALID, "corpus must be 16-byte aligned");
+  return CVS_OK;
+}
+
+int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
+
+// Scan configuration for a query block of `bq` queries at width d (false if none).
+bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
+  const int ks = ks_bucket(d);
+  switch (bq) {
+    case 16: *c = {1, 1, 1, ks}; return true;
+    case 32:
+      if (d <= 768) { *c = {1, 2, 1, ks}; return true; }
+      *c = {2, 1, 1, 48};
+      return true;
+    case 64:
+      if (d <= 384) { *c = {1, 4, 1, 12}; return true; }
+      *c = {4, 1, 2, ks};
+      return true;
+    case 128:
+      if (d <= 768) { *c = {4, 2, 2, ks}; return true; }
+      return false;
+    case 256:
+      if (d <= 384) { *c = {4, 4, 4, 12}; return true; }
+      return false;
+    default:
+      return false;
+  }
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t pow2_at_least(int64_t v) {
+  int64_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+int64_t align_up(int64_t v, int64_t a) { return ceil_div(v, a) * a; }
+
+// Reference's register-state rule (kernels.cu:499,518), kept for forced plans.
+int slots_per_lane(int64_t k) { return k <= 32 ? 1 : k <= 64 ? 2 : k <= 128 ? 4 : 8; }
+
+struct Plan {
+  bool gemv = false;
+  ScanCfg cfg{};
+  int64_t bq = 0;       // reported plan[0]
+  int64_t groups = 1;
+  int64_t chunks = 1;   // reported plan[1]
+  int64_t tile_rows = 0, ntiles = 0, tpc = 0;
+  int xcd_pair = 0;
+  int64_t nlists = 0, cap = 0;
+  // gemv
+  int64_t gemv_grid = 0, rows_per_wave = 0;
+  // sampling pre-pass
+  bool prepass = false;
+  int64_t nsample = 0, units = 0;
+  // workspace
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
+};
+
+int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t chunks, int flags,
+              int cus, Plan* p) {
+  if (k < 1 || k > 256) return fail(CVS_ERR_INVALID, "fused_topk supports 1 <= k <= 256");
+  if (k > n) return fail(CVS_ERR_INVALID, "k must not exceed the corpus size");
+  if (bq < 0) return fail(CVS_ERR_INVALID, "bq must be 0 (auto) or one of 16, 32, 64, 128, 256");
+  const bool forced_bq = bq > 0;
+  if (forced_bq) {
+    if (bq != 16 && bq != 32 && bq != 64 && bq != 128 && bq != 256)
+      return fail(CVS_ERR_INVALID, "bq must be 16, 32, 64, 128 or 256");
+    if (bq * slots_per_lane(k) > 256) return fail(CVS_ERR_INVALID, "bq * ceil(k/32) must be <= 256");
+  }
+  Plan P;
+  P.gemv = (nq == 1 && !forced_bq && !(flags & CVS_FLAG_NO_GEMV));
+  if (P.gemv) {
+    int64_t waves = chunks > 0 ? chunks : (int64_t)cus * 16;
+    waves = std::max<int64_t>(1, std::min<int64_t>({waves, kSelectMaxLists, ceil_div(n, 16)}));
+    P.gemv_grid = ceil_div(waves, 4);
+    waves = P.gemv_grid * 4;
+    P.rows_per_wave = align_up(ceil_div(n, waves), 16);
+    P.bq = 1;
+    P.chunks = waves;
+    P.nlists = waves;
+    P.cap = std::max<int64_t>(128, pow2_at_least(k + 8));
+    const int64_t nblocks = ceil_div(n, 64);
+    const int64_t s = std::min<int64_t>(1024, std::max<int64_t>(nblocks / 16, ceil_div(2 * k, 64)));
+    P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
+                (((flags & CVS_FLAG_FORCE_PREPASS) && s <= nblocks) || (s >= 4 && s <= nblocks / 8));
+    if (P.prepass) {
+      P.nsample = s;
+      P.units = s * 64;
+    }
+  } else {
+    if (!forced_bq) {
+      bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d > 384) ? 128 : 256;
+      ScanCfg tmp;
+      while (!cfg_for(bq, d, &tmp)) bq >>= 1;
+    }
+    if (!cfg_for(bq, d, &P.cfg)) return fail(CVS_ERR_INVALID, "bq=%lld is not supported at width %lld", (long long)bq, (long long)d);
+    P.bq = bq;
+    P.groups = ceil_div(std::max<int64_t>(nq, 1), bq);
+    P.tile_rows = P.cfg.tile_rows();
+    P.ntiles = ceil_div(n, P.tile_rows);
+    const int64_t rs = P.cfg.rs();
+    const int64_t max_chunks = std::min<int64_t>({P.ntiles, 65535, kSelectMaxLists / rs});
+    int64_t c;
+    if (chunks > 0) {
+      c = std::max<int64_t>(1, std::min<int64_t>(chunks, max_chunks));
+      P.tpc = ceil_div(P.ntiles, c);
+      c = ceil_div(P.ntiles, P.tpc);
+    } else {
+      c = std::max<int64_t>(1, ceil_div(cus, P.groups));
+      c = std::min<int64_t>(c, std::max<int64_t>(1, P.ntiles / 2));
+      c = std::min<int64_t>(c, max_chunks);
+      if (P.groups > 1 && c >= 8) {
+        // keep the XCD-aware mapping exact: chunk count a multiple of the 8 XCDs
+        c = std::min<int64_t>(align_up(c, 8), (max_chunks / 8) * 8);
+        P.tpc = ceil_div(P.ntiles, c);
+      } else {
+        P.tpc = ceil_div(P.ntiles, c);
+        c = ceil_div(P.ntiles, P.tpc);
+      }
+    }
+    P.chunks = c;
+    P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
+    P.nlists = c * rs;
+    P.cap = std::max<int64_t>(128, pow2_at_least(k + 16 * P.cfg.rb));
+    const int64_t upt = 4 * rs;  // sampling units per tile
+    const int64_t s = std::min<int64_t>(256, std::max<int64_t>(P.ntiles / 16, ceil_div(2 * k, upt)));
+    P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
+                (((flags & CVS_FLAG_FORCE_PREPASS) && s <= P.ntiles) || (s >= 4 && s <= P.ntiles / 8));
+    if (P.prepass) {
+      P.nsample = s;
+      P.units = s * upt;
+    }
+  }
+  if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
+  const int64_t lists = std::max<int64_t>(nq, 1) * P.nlists;
+  int64_t off = 0;
+  P.off_lv = off;
+  off = align_up(off + lists * P.cap * 4, 256);
+  P.off_li = off;
+  off = align_up(off + lists * P.cap * 4, 256);
+  P.off_cnt = off;
+  off = align_up(off + lists * 4, 256);
+  P.off_tau = off;
+  off = align_up(off + std::max<int64_t>(nq, 1) * 4, 256);
+  P.off_umax = off;
+  if (P.prepass) off = align_up(off + std::max<int64_t>(nq, 1) * P.units * 4, 256);
+  P.ws_bytes = off;
+  *p = P;
+  return CVS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cvs_version(void) { return CVS_VERSION; }
+
+const char* cvs_last_error(void) { return g_err.c_str(); }
+
+int cvs_device_supported(int device) {
+  DevInfo di;
+  if (dev_info(device, &di) != CVS_OK) return 0;
+  return di.gfx950 ? 1 : 0;
+}
+
+int cvs_fused_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t chunks,
+                   int flags, int device, int64_t* plan_out, int64_t* workspace_bytes) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
+  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  Plan P;
+  rc = make_plan(nq, n, d, k, bq, chunks, flags, di.cus, &P);
+  if (rc != CVS_OK) return rc;
+  if (plan_out) {
+    plan_out[0] = P.bq;
+    plan_out[1] = P.chunks;
+  }
+  if (workspace_bytes) *workspace_bytes = P.ws_bytes;
+  return CVS_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Records marks[i] after pipeline stage i-1 when marks != nullptr (marks[0]
+// before the first launch).  Stages: 0 sample pass, 1 threshold select, 2 scan
+// or GEMV, 3 final select; skipped stages get back-to-back marks.
+int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq,
+              int64_t chunks, int flags, void* workspace, int64_t workspace_bytes, float* out_v,
+              int32_t* out_i, int64_t* plan_out, int device, void* stream, hipEvent_t* marks) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  rc = check_inputs(q, x, nq, n, d);
+  if (rc != CVS_OK) return rc;
+  Plan P;
+  rc = make_plan(nq, n, d, k, bq, chunks, flags, di.cus, &P);
+  if (rc != CVS_OK) return rc;
+  if (plan_out) {
+    plan_out[0] = P.bq;
+    plan_out[1] = P.chunks;
+  }
+  if (nq == 0) return CVS_OK;
+  if (out_v == nullptr || out_i == nullptr) return fail(CVS_ERR_INVALID, "output pointers must not be null");
+  if (workspace == nullptr || workspace_bytes < P.ws_bytes)
+    return fail(CVS_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)P.ws_bytes,
+                (long long)workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(CVS_ERR_INVALID, "workspace must be 256-byte aligned");
+
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto mark = [&](int i) {
+    if (marks) (void)hipEventRecord(marks[i], s);
+  };
+  mark(0);
+  char* ws = static_cast<char*>(workspace);
+  float* lv = reinterpret_cast<float*>(ws + P.off_lv);
+  int* li = reinterpret_cast<int*>(ws + P.off_li);
+  int* cnt = reinterpret_cast<int*>(ws + P.off_cnt);
+  float* tau = reinterpret_cast<float*>(ws + P.off_tau);
+  float* umax = reinterpret_cast<float*>(ws + P.off_umax);
+  const _Float16* qh = static_cast<const _Float16*>(q);
+  const _Float16* xh = static_cast<const _Float16*>(x);
+  hipError_t e;
+
+  if (P.gemv) {
+    GemvArgs g{};
+    g.q = qh;
+    g.x = xh;
+    g.n = n;
+    g.d = (int)d;
+    g.rows_per_wave = P.rows_per_wave;
+    g.k = (int)k;
+    g.cap = (int)P.cap;
+    if (P.prepass) {
+      GemvArgs pg = g;
+      pg.mode = kMax;
+      pg.umax = umax;
+      pg.nsample = (int)P.nsample;
+      pg.units = (int)P.units;
+      e = launch_gemv(ks_bucket(d) * 32, pg, (int)ceil_div(P.nsample, 4), s);
+      if (e != hipSuccess) return hip_fail(e, "gemv sample pass launch");
+      SelectArgs sa{};
+      sa.lv = umax;
+      sa.nlists = 1;
+      sa.cap = (int)P.units;
+      sa.k = (int)k;
+      sa.tau = tau;
+      mark(1);
+      e = launch_select(1, sa, 1, s);
+      if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+      mark(2);
+      g.tau = tau;
+    } else {
+      mark(1);
+      mark(2);
+    }
+    g.mode = kAppend;
+    g.lv = lv;
+    g.li = li;
+    g.lcount = cnt;
+    g.nlists = (int)P.nlists;
+    e = launch_gemv(ks_bucket(d) * 32, g, (int)P.gemv_grid, s);
+    if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    mark(3);
+  } else {
+    ScanArgs a{};
+    a.q = qh;
+    a.x = xh;
+    a.n = n;
+    a.nq = (int)nq;
+    a.d = (int)d;
+    a.groups = (int)P.groups;
+    a.nchunks = (int)P.chunks;
+    a.ntiles = P.ntiles;
+    a.tpc = P.tpc;
+    a.xcd_pair = P.xcd_pair;
+    a.k = (int)k;
+    a.cap = (int)P.cap;
+    if (P.prepass) {
+      ScanArgs pa = a;
+      pa.umax = umax;
+      pa.nsample = (int)P.nsample;
+      pa.units = (int)P.units;
+      e = launch_scan(P.cfg, kMax, pa, (int)(P.groups * P.nsample), s);
+      if (e != hipSuccess) return hip_fail(e, "sample pass launch");
+      SelectArgs sa{};
+      sa.lv = umax;
+      sa.nlists = 1;
+      sa.cap = (int)P.units;
+      sa.k = (int)k;
+      sa.tau = tau;
+      mark(1);
+      e = launch_select(1, sa, (int)nq, s);
+      if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+      mark(2);
+      a.tau = tau;
+    } else {
+      mark(1);
+      mark(2);
+    }
+    a.lv = lv;
+    a.li = li;
+    a.lcount = cnt;
+    a.nlists = (int)P.nlists;
+    e = launch_scan(P.cfg, kAppend, a, (int)(P.groups * P.chunks), s);
+    if (e != hipSuccess) return hip_fail(e, "scan launch");
+    mark(3);
+  }
+  SelectArgs fa{};
+  fa.lv = lv;
+  fa.li = li;
+  fa.lcount = cnt;
+  fa.nlists = (int)P.nlists;
+  fa.cap = (int)P.cap;
+  fa.k = (int)k;
+  fa.out_v = out_v;
+  fa.out_i = out_i;
+  e = launch_select(0, fa, (int)nq, s);
+  if (e != hipSuccess) return hip_fail(e, "select launch");
+  mark(4);
+  return CVS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cvs_fused_topk(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                   int64_t bq, int64_t chunks, int flags, void* workspace, int64_t workspace_bytes,
+                   float* out_v, int32_t* out_i, int64_t* plan_out, int device, void* stream) {
+  return run_fused(q, x, nq, n, d, k, bq, chunks, flags, workspace, workspace_bytes, out_v, out_i,
+                   plan_out, device, stream, nullptr);
+}
+
+int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                         int64_t bq, int64_t chunks, int flags, void* workspace,
+                         int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                         int device, void* stream, float* stage_ms) {
+  if (stage_ms == nullptr) return fail(CVS_ERR_INVALID, "stage_ms must not be null");
+  for (int i = 0; i < 4; ++i) stage_ms[i] = 0.f;
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipEvent_t ev[5] = {};
+  for (int i = 0; i < 5; ++i) {
+    hipError_t e = hipEventCreate(&ev[i]);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      return hip_fail(e, "hipEventCreate");
+    }
+  }
+  int rc = run_fused(q, x, nq, n, d, k, bq, chunks, flags, workspace, workspace_bytes, out_v, out_i,
+                     plan_out, device, stream, nq > 0 ? ev : nullptr);
+  if (rc == CVS_OK && nq > 0) {
+    hipError_t e = hipEventSynchronize(ev[4]);
+    if (e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
+    for (int i = 0; rc == CVS_OK && i < 4; ++i) {
+      e = hipEventElapsedTime(&stage_ms[i], ev[i], ev[i + 1]);
+      if (e != hipSuccess) rc = hip_fail(e, "hipEventElapsedTime");
+    }
+  }
+  for (int i = 0; i < 5; ++i) (void)hipEventDestroy(ev[i]);
+  return rc;
+}
+
+int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, void* out, int out_fp32,
+               int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  rc = check_inputs(q, x, nq, n, d);
+  if (rc != CVS_OK) return rc;
+  if (nq == 0 || n == 0) return CVS_OK;
+  if (out == nullptr) return fail(CVS_ERR_INVALID, "output pointer must not be null");
+  ScanCfg cfg;
+  cfg_for(nq <= 16 ? 16 : 64, d, &cfg);
+  const int64_t bq = cfg.bq();
+  const int64_t groups = ceil_div(nq, bq);
+  const int64_t ntiles = ceil_div(n, cfg.tile_rows());
+  int64_t c = std::max<int64_t>(1, ceil_div(2 * (int64_t)di.cus, groups));
+  c = std::min<int64_t>({c, ntiles, 65535});
+  const int64_t tpc = ceil_div(ntiles, c);
+  c = ceil_div(ntiles, tpc);
+  if (groups * c > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
+
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  ScanArgs a{};
+  a.q = static_cast<const _Float16*>(q);
+  a.x = static_cast<const _Float16*>(x);
+  a.n = n;
+  a.nq = (int)nq;
+  a.d = (int)d;
+  a.groups = (int)groups;
+  a.nchunks = (int)c;
+  a.ntiles = ntiles;
+  a.tpc = tpc;
+  a.out = out;
+  hipError_t e = launch_scan(cfg, out_fp32 ? kStoreF32 : kStoreF16, a, (int)(groups * c),
+                             reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "score kernel launch");
+  return CVS_OK;
+}
+
+}  // extern "C"

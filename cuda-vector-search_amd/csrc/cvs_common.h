@@ -1,0 +1,125 @@
+// Shared device helpers for the gfx950 exact top-k engine.
+//
+// Candidate encoding: a (score, row id) pair is packed into one 64-bit key whose
+// unsigned order is the search's total order: score descending, then id
+// ascending (the order the reference emits, csrc/kernels.cu:277-279).  Keys are
+// unique per query because row ids are, so "the k largest keys" is exactly the
+// top-k, ties included.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cvs {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // 4 waves, one per SIMD
+
+// ---- 64-bit search keys ----------------------------------------------------
+
+__device__ __forceinline__ uint32_t float_order(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float order_float(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+__device__ __forceinline__ uint64_t make_key(float v, int id) {
+  return ((uint64_t)float_order(v) << 32) | (uint64_t)(~(uint32_t)id);
+}
+
+__device__ __forceinline__ float key_score(uint64_t key) { return order_float((uint32_t)(key >> 32)); }
+__device__ __forceinline__ int key_id(uint64_t key) { return (int)(~(uint32_t)key); }
+
+// ---- s_waitcnt encodings (gfx9 family: vmcnt is 6 bits split 3:0 / 15:14) ----
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4));
+}
+
+// ---- wave utilities ---------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int coherent_load(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sorts keys[0..N) descending in LDS; N is a power of two.  Called by one whole
+// wave; LDS operations of a wave are performed in issue order, and the
+// wavefront fence keeps the compiler from reordering them across stages.
+__device__ __forceinline__ void wave_lds_sort_desc(uint64_t* keys, int N) {
+  const int lane = lane_id();
+#pragma unroll 1
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll 1
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll 1
+      for (int i = lane; i < (N >> 1); i += kWave) {
+        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = ((lo & size) == 0);
+        const uint64_t a = keys[lo], b = keys[hi];
+        if (desc ? (a < b) : (a > b)) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+  }
+}
+
+// Shrinks one candidate list (owned by the calling wave; `count` entries at
+// lv/li) to its k best entries, in place, and returns the score of the k-th
+// best: a lower bound on the k-th best score of everything the list has been
+// offered, hence a valid filter for later candidates.  `scratch` is this wave's
+// private LDS area of at least next_pow2(count) keys.  Called by all 64 lanes
+// with identical arguments.  Requires 1 <= k <= count.
+__device__ __forceinline__ float wave_compact(float* lv, int* li, int count, int k, uint64_t* scratch) {
+  const int lane = lane_id();
+  // The list was written by this wave's own global stores: wait for them, and
+  // read it back past the (non-coherent) vector L1.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  int N = 2;
+  while (N < count) N <<= 1;
+#pragma unroll 1
+  for (int p = lane; p < N; p += kWave)
+    scratch[p] = (p < count) ? make_key(coherent_load(lv + p), coherent_load(li + p)) : 0ull;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  wave_lds_sort_desc(scratch, N);
+#pragma unroll 1
+  for (int p = lane; p < k; p += kWave) {
+    const uint64_t key = scratch[p];
+    lv[p] = key_score(key);
+    li[p] = key_id(key);
+  }
+  const float kth = key_score(scratch[k - 1]);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  return kth;
+}
+
+}  // namespace cvs

@@ -1,0 +1,101 @@
+// Host-visible kernel argument blocks and launchers (internal to libcvs_hip.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cvs {
+
+// What the scan kernel does with each score tile.
+enum ScanMode : int {
+  kAppend = 0,    // filter against a threshold, append survivors to per-wave candidate lists
+  kMax = 1,       // sample pass: per-(query, unit) maxima over disjoint row sets
+  kStoreF32 = 2,  // write the full score matrix (fp32)
+  kStoreF16 = 3,  // write the full score matrix (fp16)
+};
+
+// One tile of corpus rows is scored against a group of queries by one
+// 256-thread workgroup.  Queries are split across the 4 waves (QS ways) and the
+// tile's rows across the rest (RS = 4/QS ways).  Queries stay in VGPRs for the
+// whole launch; the corpus streams through LDS in 64-column stages.
+struct ScanArgs {
+  const _Float16* q;  // [nq, d] fp16, row-major, d % 64 == 0
+  const _Float16* x;  // [n, d]  fp16, row-major
+  int64_t n;
+  int nq;
+  int d;
+  int groups;         // query groups (gridwise); group g owns queries [g*bq, (g+1)*bq)
+  int nchunks;        // corpus chunks per query group
+  int64_t ntiles;     // ceil(n / tile_rows)
+  int64_t tpc;        // tiles per chunk
+  int xcd_pair;       // 1: map workgroups so a chunk's query groups share an XCD
+  // kAppend
+  const float* tau;   // [nq] initial thresholds, or null for -inf
+  float* lv;          // [nq, nlists, cap] candidate scores
+  int* li;            // [nq, nlists, cap] candidate row ids
+  int* lcount;        // [nq, nlists]
+  int nlists;         // nchunks * RS
+  int cap;            // list capacity (power of two, >= k + rows per wave per tile)
+  int k;
+  // kMax
+  float* umax;        // [nq, units]
+  int nsample;        // sampled tiles (one per workgroup)
+  int units;          // units per query = nsample * RS * 4
+  // kStore*
+  void* out;          // [nq, n]
+};
+
+// Batch-1 GEMV: one query, rows split across waves, 8 lanes per row.
+struct GemvArgs {
+  const _Float16* q;  // [1, d]
+  const _Float16* x;  // [n, d]
+  int64_t n;
+  int d;
+  int64_t rows_per_wave;
+  const float* tau;   // [1] or null
+  float* lv;
+  int* li;
+  int* lcount;        // [nlists]
+  int nlists;         // total waves
+  int cap;
+  int k;
+  float* umax;        // kMax: [units], one unit per sampled row
+  int nsample;        // kMax: sampled 64-row blocks (one per wave)
+  int units;
+  int mode;           // kAppend or kMax
+};
+
+// Exact selection over candidate lists: one workgroup per query.
+struct SelectArgs {
+  const float* lv;     // [nq, nlists, cap]
+  const int* li;       // [nq, nlists, cap] or null (id = flat position)
+  const int* lcount;   // [nq, nlists] or null (every list holds `cap` entries)
+  int nlists;
+  int cap;
+  int k;
+  float* out_v;        // [nq, k] (final mode)
+  int* out_i;          // [nq, k] (final mode)
+  float* tau;          // [nq]    (threshold mode: score of the k-th best)
+};
+
+// Scan configurations (queries per wave QW = 16*QB; tile rows = RS*RB*16).
+struct ScanCfg {
+  int qs, qb, rb, ksmax;
+  int bq() const { return qs * 16 * qb; }
+  int rs() const { return 4 / qs; }
+  int tile_rows() const { return rs() * rb * 16; }
+  int wave_rows() const { return rb * 16; }
+  int dmax() const { return ksmax * 32; }
+};
+
+// Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).
+hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
+hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
+hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s);
+
+bool scan_cfg_available(const ScanCfg& cfg, int mode);
+
+constexpr int kSelectMaxLists = 8192;
+constexpr int kMaxCap = 512;  // largest candidate-list capacity (k <= 256)
+
+}  // namespace cvs

@@ -1,0 +1,221 @@
+"""Loader for the gfx950 engine ``libcvs_hip.so`` (C ABI, see include/cvs.h).
+
+Drop-in for the reference's ``cuda_vector_search/_ext.py:15-47``: the same two
+functions, ``available()`` and ``load(verbose=False)``, and ``load()`` returns an
+object with the reference extension's methods
+
+    scores(q, x, out_fp32=True) -> Tensor[nq, n]                 (kernels.cu:472-497)
+    fused_topk(q, x, k, bq=0, chunks=0) -> [v, i, plan]          (kernels.cu:501-582)
+
+with the reference's argument checks and ``RuntimeError`` messages
+(kernels.cu:451-470).  Underneath, torch only supplies device memory and the
+current stream; every score and every selection is computed by the HIP
+kernels.  There is no fallback inside this module: if the library cannot be
+loaded on a GPU that ``available()`` accepts, ``load()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+_lock = threading.Lock()
+_mod = None
+
+LIBRARY = Path(__file__).with_name("libcvs_hip.so")
+ARCH = "gfx950"
+
+# Flags of cvs_fused_topk (include/cvs.h).
+FLAG_NO_PREPASS = 1
+FLAG_FORCE_PREPASS = 2
+FLAG_NO_GEMV = 4
+
+
+def available() -> bool:
+    """True when the current torch device is an MI355X-class (gfx950) GPU."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return False
+    try:
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+    except Exception:  # pragma: no cover - exotic torch builds
+        return False
+    return str(arch).split(":")[0] == ARCH
+
+
+def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
+    i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+    lib.cvs_version.restype = i32
+    lib.cvs_version.argtypes = []
+    lib.cvs_last_error.restype = ctypes.c_char_p
+    lib.cvs_last_error.argtypes = []
+    lib.cvs_device_supported.restype = i32
+    lib.cvs_device_supported.argtypes = [i32]
+    lib.cvs_scores.restype = i32
+    lib.cvs_scores.argtypes = [vp, vp, i64, i64, i64, vp, i32, i32, vp]
+    lib.cvs_fused_plan.restype = i32
+    lib.cvs_fused_plan.argtypes = [i64, i64, i64, i64, i64, i64, i32, i32,
+                                   ctypes.POINTER(i64), ctypes.POINTER(i64)]
+    lib.cvs_fused_topk.restype = i32
+    lib.cvs_fused_topk.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
+                                   vp, vp, ctypes.POINTER(i64), i32, vp]
+    lib.cvs_fused_topk_timed.restype = i32
+    lib.cvs_fused_topk_timed.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
+                                         vp, vp, ctypes.POINTER(i64), i32, vp,
+                                         ctypes.POINTER(ctypes.c_float)]
+    return lib
+
+
+def open_library(path: str | Path | None = None) -> ctypes.CDLL:
+    """ctypes handle of the engine library with its signatures bound (no GPU needed)."""
+    return _bind(ctypes.CDLL(str(path or LIBRARY)))
+
+
+class Engine:
+    """The object ``load()`` returns: the reference extension's two methods."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self.lib = lib
+        self.path = str(LIBRARY)
+
+    # -- helpers -------------------------------------------------------------
+    def _error(self, rc: int) -> RuntimeError:
+        msg = self.lib.cvs_last_error().decode("utf-8", "replace")
+        return RuntimeError(msg or f"libcvs_hip error {rc}")
+
+    @staticmethod
+    def _check_matrix(t, name: str) -> None:
+        import torch
+
+        if not (isinstance(t, torch.Tensor) and t.is_cuda):
+            raise RuntimeError(f"{name} must be a CUDA tensor")
+        if t.dtype != torch.float16:
+            raise RuntimeError(f"{name} must be float16")
+        if t.dim() != 2:
+            raise RuntimeError(f"{name} must be 2-D")
+        if not t.is_contiguous():
+            raise RuntimeError(f"{name} must be contiguous")
+        if t.shape[1] % 64 != 0:
+            raise RuntimeError(f"{name} width must be a multiple of 64 (zero-pad it)")
+        if t.data_ptr() % 16 != 0:
+            raise RuntimeError(f"{name} must be 16-byte aligned")
+
+    def _check_pair(self, q, x) -> None:
+        self._check_matrix(q, "queries")
+        self._check_matrix(x, "corpus")
+        if q.device != x.device:
+            raise RuntimeError("queries and corpus must be on the same device")
+        if q.shape[1] != x.shape[1]:
+            raise RuntimeError("queries and corpus must have the same width")
+        if x.shape[0] >= 2**31 - 1:
+            raise RuntimeError("corpus must have fewer than 2^31 rows")
+        if q.shape[0] >= 2**31 - 1:
+            raise RuntimeError("too many queries")
+
+    @staticmethod
+    def _stream(dev):
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    # -- reference API -------------------------------------------------------
+    def scores(self, q, x, out_fp32: bool = True):
+        import torch
+
+        self._check_pair(q, x)
+        nq, d = q.shape
+        n = x.shape[0]
+        out = torch.empty((nq, n), dtype=torch.float32 if out_fp32 else torch.float16, device=q.device)
+        if nq == 0 or n == 0:
+            return out
+        rc = self.lib.cvs_scores(q.data_ptr(), x.data_ptr(), nq, n, d, out.data_ptr(),
+                                 1 if out_fp32 else 0, q.device.index, self._stream(q.device))
+        if rc != 0:
+            raise self._error(rc)
+        return out
+
+    def plan(self, nq: int, n: int, d: int, k: int, bq: int = 0, chunks: int = 0, flags: int = 0,
+             device: int = 0):
+        """(plan[2], workspace_bytes) for these sizes, without running anything."""
+        plan = (ctypes.c_int64 * 2)()
+        ws = ctypes.c_int64(0)
+        rc = self.lib.cvs_fused_plan(nq, n, d, k, bq, chunks, flags, device, plan, ctypes.byref(ws))
+        if rc != 0:
+            raise self._error(rc)
+        return [int(plan[0]), int(plan[1])], int(ws.value)
+
+    def fused_topk(self, q, x, k: int, bq: int = 0, chunks: int = 0, flags: int = 0):
+        return self._fused(q, x, k, bq, chunks, flags, None)
+
+    def fused_topk_timed(self, q, x, k: int, bq: int = 0, chunks: int = 0, flags: int = 0):
+        """fused_topk plus per-stage device milliseconds (HIP events on the current
+        stream): [sample pass, threshold select, scan/GEMV, final select].  Blocks."""
+        ms = (ctypes.c_float * 4)()
+        out = self._fused(q, x, k, bq, chunks, flags, ms)
+        return out, [float(v) for v in ms]
+
+    def _fused(self, q, x, k, bq, chunks, flags, stage_ms):
+        import torch
+
+        self._check_pair(q, x)
+        nq, d = q.shape
+        n = x.shape[0]
+        k, bq, chunks = int(k), int(bq), int(chunks)
+        dev = q.device
+        plan_c = (ctypes.c_int64 * 2)()
+        ws_bytes = ctypes.c_int64(0)
+        rc = self.lib.cvs_fused_plan(nq, n, d, k, bq, chunks, flags, dev.index, plan_c,
+                                     ctypes.byref(ws_bytes))
+        if rc != 0:
+            raise self._error(rc)
+        out_v = torch.empty((nq, k), dtype=torch.float32, device=dev)
+        out_i = torch.empty((nq, k), dtype=torch.int32, device=dev)
+        plan = torch.tensor([int(plan_c[0]), int(plan_c[1])], dtype=torch.int64)
+        if nq == 0:
+            return [out_v, out_i, plan]
+        ws = torch.empty(max(int(ws_bytes.value), 256), dtype=torch.uint8, device=dev)
+        args = (q.data_ptr(), x.data_ptr(), nq, n, d, k, bq, chunks, flags, ws.data_ptr(), ws.numel(),
+                out_v.data_ptr(), out_i.data_ptr(), plan_c, dev.index, self._stream(dev))
+        if stage_ms is None:
+            rc = self.lib.cvs_fused_topk(*args)
+        else:
+            rc = self.lib.cvs_fused_topk_timed(*args, stage_ms)
+        if rc != 0:
+            raise self._error(rc)
+        return [out_v, out_i, plan]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libcvs_hip.so in-tree (hipcc, gfx950)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "_cvs_build", Path(__file__).resolve().parent.parent / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build(verbose=verbose)
+
+
+def load(verbose: bool = False) -> Engine:
+    """Load (building once if the library is missing) and return the engine."""
+    global _mod
+    if _mod is not None:
+        return _mod
+    with _lock:
+        if _mod is not None:
+            return _mod
+        if not available():
+            raise RuntimeError("cuda-vector-search kernels need an AMD Instinct MI355X (gfx950) GPU")
+        if not LIBRARY.exists():
+            build(verbose)
+        lib = open_library()
+        import torch
+
+        dev = torch.cuda.current_device()
+        if not lib.cvs_device_supported(dev):
+            raise RuntimeError(f"libcvs_hip does not support device {dev}: "
+                               + lib.cvs_last_error().decode("utf-8", "replace"))
+        _mod = Engine(lib)
+        return _mod

@@ -1,0 +1,158 @@
+"""``Index``: exact top-k search over an fp16 corpus resident in GPU memory.
+
+Public behaviour is that of the reference's ``cuda_vector_search/index.py:44-155``
+(constructor arguments, copy/aliasing rules, in-place cosine normalisation,
+zero-padding of the width to a multiple of 64, method dispatch, error types and
+messages, ``.npy`` + ``<path>.json`` persistence).  The difference is underneath:
+``method="fused"``/``"twopass"`` and ``scores()`` run the gfx950 HIP engine
+(``libcvs_hip.so`` through ``_ext``), never a CUDA extension.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _ext
+from .reference import torch_topk
+
+PAD = 64            # widths are zero-padded to a multiple of this (the MFMA depth step x 2)
+MAX_FUSED_K = 256   # largest k of the fused path
+MAX_KERNEL_WIDTH = 1536  # widest (padded) rows the gfx950 kernels accept
+_NORM_CHUNK = 1 << 18
+
+METHODS = ("auto", "fused", "twopass", "torch")
+
+
+def _as_tensor(a) -> torch.Tensor:
+    return a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))
+
+
+def _padded(x: torch.Tensor) -> torch.Tensor:
+    """Zero-pad the columns up to the next multiple of PAD (no copy when already aligned)."""
+    extra = (-x.shape[1]) % PAD
+    return torch.nn.functional.pad(x, (0, extra)) if extra else x
+
+
+def _normalize_(x: torch.Tensor) -> torch.Tensor:
+    """Unit-normalise the rows of ``x`` in place, converting at most 2^18 rows to fp32 at a time."""
+    n = x.shape[0]
+    for lo in range(0, n, _NORM_CHUNK):
+        rows = x[lo:lo + _NORM_CHUNK]
+        f = rows.float()
+        f = f / f.norm(dim=1, keepdim=True).clamp_min(1e-12)
+        rows.copy_(f.to(x.dtype))
+    return x
+
+
+class Index:
+    """Brute-force (exact) top-k index.
+
+    Args:
+        embeddings: ``[n, d]`` array or tensor; stored as fp16 on a GPU, fp32 on the CPU.
+        metric: ``"cosine"`` (rows and queries are L2-normalised) or ``"ip"``.
+        device: ``"cuda"``, ``"cuda:1"``, ``"cpu"``...; defaults to the GPU when present.
+        copy: with ``False`` a contiguous fp16 tensor already on the device is stored
+            without a copy (and normalised in place for cosine).
+    """
+
+    def __init__(self, embeddings, metric: str = "cosine", device=None, copy: bool = True):
+        if metric not in ("cosine", "ip"):
+            raise ValueError("metric must be 'cosine' or 'ip'")
+        src = _as_tensor(embeddings)
+        if src.dim() != 2:
+            raise ValueError("embeddings must be 2-D [n, d]")
+        if src.shape[0] == 0:
+            raise ValueError("embeddings is empty")
+        self.device = torch.device(device if device is not None else
+                                   ("cuda" if torch.cuda.is_available() else "cpu"))
+        self.metric = metric
+        self.dim = int(src.shape[1])
+        on_gpu = self.device.type == "cuda"
+
+        x = src.to(self.device, torch.float16 if on_gpu else torch.float32)
+        if copy and x.data_ptr() == src.data_ptr():  # .to() returned the caller's storage
+            x = x.clone()
+        x = x.contiguous()
+        if metric == "cosine":
+            _normalize_(x)
+        self._x = _padded(x) if on_gpu else x
+        self._use_kernels = on_gpu and _ext.available()
+
+    # -- basics -------------------------------------------------------------
+    def __len__(self) -> int:
+        return int(self._x.shape[0])
+
+    @property
+    def embeddings(self) -> torch.Tensor:
+        """The stored matrix (normalised for cosine), without the padding columns."""
+        return self._x[:, :self.dim]
+
+    def _prep_queries(self, queries) -> torch.Tensor:
+        q = _as_tensor(queries)
+        if q.dim() == 1:
+            q = q.unsqueeze(0)
+        if q.dim() != 2 or q.shape[1] != self.dim:
+            raise ValueError(f"queries must be [b, {self.dim}]")
+        q = q.to(self.device, self._x.dtype).contiguous()
+        if self.metric == "cosine":
+            q = _normalize_(q.clone())
+        return _padded(q) if self.device.type == "cuda" else q
+
+    # -- search -------------------------------------------------------------
+    def search(self, queries, k: int = 10, method: str = "auto"):
+        """Top-k (scores ``[b, k]`` float32, ids ``[b, k]`` int64), best first.
+
+        method:
+            "fused"   - gfx950 engine: MFMA scores + threshold filter + exact select (k <= 256)
+            "twopass" - gfx950 score kernel writes the fp16 matrix, then torch.topk
+            "torch"   - torch matmul + torch.topk
+            "auto"    - fused when possible, else torch
+        """
+        if method not in METHODS:
+            raise ValueError(f"method must be one of {METHODS}")
+        k = int(k)
+        if k < 1:
+            raise ValueError("k must be >= 1")
+        k = min(k, len(self))
+        q = self._prep_queries(queries)
+        if method == "auto":
+            fits = k <= MAX_FUSED_K and self._x.shape[1] <= MAX_KERNEL_WIDTH
+            method = "fused" if (self._use_kernels and fits) else "torch"
+        if method in ("fused", "twopass") and not self._use_kernels:
+            raise RuntimeError(f"method={method!r} needs an AMD Instinct MI355X (gfx950) GPU")
+        if method == "fused":
+            if k > MAX_FUSED_K:
+                raise ValueError(f"fused search supports k <= {MAX_FUSED_K}")
+            v, i, _ = _ext.load().fused_topk(q, self._x, k)
+            return v, i.long()
+        if method == "twopass":
+            s = _ext.load().scores(q, self._x, False)
+            v, i = torch.topk(s, k, dim=1)
+            return v.float(), i
+        return torch_topk(q, self._x, k)
+
+    def scores(self, queries, fp32: bool = True) -> torch.Tensor:
+        """Full ``[b, n]`` score matrix (gfx950 score kernel on a GPU index)."""
+        q = self._prep_queries(queries)
+        if not self._use_kernels:
+            return (q @ self._x.T).float()
+        return _ext.load().scores(q, self._x, fp32)
+
+    # -- persistence --------------------------------------------------------
+    def save(self, path) -> None:
+        """Write the stored vectors to ``path`` (``np.save``, fp16) and ``<path>.json`` metadata."""
+        path = Path(path)
+        np.save(path, self.embeddings.to(torch.float16).cpu().numpy())
+        Path(f"{path}.json").write_text(json.dumps({"metric": self.metric, "dim": self.dim, "n": len(self)}))
+
+    @classmethod
+    def load(cls, path, metric: str | None = None, device=None) -> "Index":
+        path = Path(path)
+        if metric is None:
+            side = Path(f"{path}.json")
+            metric = json.loads(side.read_text())["metric"] if side.exists() else "cosine"
+        return cls(torch.from_numpy(np.load(path)), metric=metric, device=device, copy=False)

@@ -1,0 +1,113 @@
+/*
+ * C ABI of libcvs_hip.so, the gfx950 (MI355X) exact top-k search engine.
+ *
+ * This is the drop-in boundary for the hot path of cuda-vector-search.  The
+ * reference exposes two functions through a pybind11 extension
+ * (cuda_vector_search/csrc/kernels.cu:586-592) that its Python layer calls
+ * through _ext.load() (cuda_vector_search/_ext.py:24-47):
+ *
+ *     scores(q, x, out_fp32=True)                 kernels.cu:472-497
+ *     fused_topk(q, x, k, bq=0, chunks=0)         kernels.cu:501-582
+ *
+ * Here the same two operations are plain C functions over raw device
+ * pointers, so any FFI (ctypes, cffi, cgo, JNI) can bind them.  No torch types
+ * appear in the signatures.  Conventions shared by every entry point:
+ *
+ *   - q is [nq, d] and x is [n, d], fp16 (IEEE binary16), row-major,
+ *     contiguous, 16-byte aligned, on `device`; d is a multiple of 64 (the
+ *     caller zero-pads, as index.py:27-32 does) and at most 1536.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Work is enqueued
+ *     asynchronously on it; no entry point synchronises or allocates device
+ *     memory.  Results are valid once the stream reaches them.
+ *   - The return value is CVS_OK (0) or an error code; cvs_last_error() then
+ *     returns a message for the calling thread (the reference raises
+ *     RuntimeError with the same wording via TORCH_CHECK, kernels.cu:451-470,
+ *     509-518).
+ *   - Entry points are thread-safe and re-entrant (no global mutable state
+ *     other than an init-once cache of device properties).
+ */
+#ifndef CVS_H_
+#define CVS_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CVS_VERSION 100 /* 0.1.0; the Python package's __version__ mirrors it */
+
+#define CVS_OK 0
+#define CVS_ERR_INVALID 1 /* bad argument: the reference's TORCH_CHECK failures */
+#define CVS_ERR_HIP 2     /* HIP runtime / launch error */
+
+/* fused_topk flags (0 = the default plan).  Test and tuning knobs. */
+#define CVS_FLAG_NO_PREPASS 1    /* skip the sampling pre-pass (threshold starts at -inf) */
+#define CVS_FLAG_FORCE_PREPASS 2 /* run the pre-pass whenever it is well defined */
+#define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
+
+/* Library version (CVS_VERSION). */
+int cvs_version(void);
+
+/* Message for the last error on the calling thread ("" if none). */
+const char* cvs_last_error(void);
+
+/* 1 if `device` is a gfx950 GPU this library can run on, else 0.
+ * Replaces the capability gate of _ext.py:15-21 / kernels.cu:468-469. */
+int cvs_device_supported(int device);
+
+/*
+ * Full score matrix out[i, r] = sum_j q[i, j] * x[r, j], fp32 accumulation.
+ * out is [nq, n], fp32 when out_fp32 != 0, else fp16 (rounded to nearest).
+ * Replaces scores() of kernels.cu:472-497 (Index.scores, index.py:133-138, and
+ * the "twopass" method, index.py:127-130).
+ */
+int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, void* out,
+               int out_fp32, int device, void* stream);
+
+/*
+ * Plan of cvs_fused_topk for these sizes, without running it.
+ * plan_out[0] = query-block size (the reference's bq; 1 for the batch-1 GEMV
+ * path), plan_out[1] = corpus chunks (lists per query for the GEMV path);
+ * *workspace_bytes = device scratch the call needs.  Replaces the plan
+ * heuristic of kernels.cu:499-536.  bq = 0 / chunks = 0 mean "auto"; a forced
+ * bq must be 16, 32, 64, 128 or 256 and, as in the reference, satisfy
+ * bq * slots(k) <= 256 with slots(k) = 1/2/4/8 for k <= 32/64/128/256; a forced
+ * chunks >= 1 is clamped to what the corpus allows.
+ */
+int cvs_fused_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t chunks,
+                   int flags, int device, int64_t* plan_out, int64_t* workspace_bytes);
+
+/*
+ * Exact top-k by inner product: for each query, the k rows with the largest
+ * fp32-accumulated score, sorted by score descending and then row id
+ * ascending.  out_v is [nq, k] fp32, out_i is [nq, k] int32.  Requires
+ * 1 <= k <= 256 and k <= n.  `workspace` (256-byte aligned) must hold at least
+ * the bytes cvs_fused_plan reports for the same arguments; its contents need
+ * no initialisation.  plan_out (may be NULL) receives the plan as in
+ * cvs_fused_plan.  Replaces fused_topk() of kernels.cu:501-582 (Index.search
+ * method "fused", index.py:123-126).
+ */
+int cvs_fused_topk(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                   int64_t bq, int64_t chunks, int flags, void* workspace, int64_t workspace_bytes,
+                   float* out_v, int32_t* out_i, int64_t* plan_out, int device, void* stream);
+
+/*
+ * Diagnostic twin of cvs_fused_topk (no counterpart in the reference): runs
+ * exactly the same launches, records a HIP event on `stream` between them,
+ * waits for the last one and writes the elapsed milliseconds of each pipeline
+ * stage to stage_ms[0..3]: sampling pre-pass, threshold select, scan (or
+ * batch-1 GEMV), final select (0 for a stage the plan skips).  Used by the
+ * benchmark to time the dominant kernel on the stream it runs on.  Unlike
+ * cvs_fused_topk it blocks until the work is done.
+ */
+int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                         int64_t bq, int64_t chunks, int flags, void* workspace,
+                         int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                         int device, void* stream, float* stage_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CVS_H_ */

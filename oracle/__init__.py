@@ -1,0 +1,224 @@
+"""CPU oracle for the exact top-k hot path.  TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker or the timed CPU
+baseline.  The shipped package (``cuda-vector-search_amd/cuda_vector_search``)
+never imports it; its HIP path fails loudly instead of falling back here.
+
+Contents, each restating one reference function (file:line into the reference):
+
+* ``topk`` / ``scores``  - C restatement (``cvs_oracle.c``) of
+  ``cuda_vector_search/reference.py:18-34`` (exact fp32 top-k over the stored
+  fp16 values) with the total output order of ``csrc/kernels.cu:277-279``
+  (score desc, id asc), and of the score matrix of ``csrc/kernels.cu:472-497``.
+* ``exact_topk_fp32``    - numpy restatement of ``reference.py:18-34`` (chunked
+  fp32 matmul + running top-k merge), ties ordered by id.
+* ``torch_topk_cpu``     - the reference's CPU torch path ``reference.py:8-15``
+  (fp32 ``q @ x.T`` + ``torch.topk``), used as a CPU baseline.
+* ``numpy_search``       - ``bench/bench_baselines.py:45-50`` (matmul +
+  argpartition + argsort), used as a CPU baseline.
+* ``check_exact``        - the acceptance rule of ``tests/test_search.py:21-44``
+  plus the id-parity rule (ids identical except inside the near-tie band of the
+  k-th score).
+
+Pinning (see ``tests/test_oracle.py``): fp16 decoding is checked exhaustively
+against numpy; ``topk`` is checked against committed golden vectors made by an
+independent float64 brute force (``tests/golden/make_golden.py``), against the
+closed forms k=1 (arg-max), k=n (full sort), identity corpora (score = query
+coordinate), exact duplicates (ties by id) and planted mistakes that
+``check_exact`` must reject.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import numpy as np
+
+_DIR = Path(__file__).resolve().parent
+_LIB_PATH = _DIR / "libcvs_oracle.so"
+_lock = threading.Lock()
+_lib = None
+
+
+def build(force: bool = False) -> Path:
+    """Compile ``libcvs_oracle.so`` with the Makefile beside this file."""
+    import subprocess
+
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(_DIR), "-B" if force else "all"], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not _LIB_PATH.exists():
+                build()
+            L = ctypes.CDLL(str(_LIB_PATH))
+            L.cvs_oracle_half_to_float.restype = ctypes.c_float
+            L.cvs_oracle_half_to_float.argtypes = [ctypes.c_uint16]
+            L.cvs_oracle_topk.restype = ctypes.c_int
+            L.cvs_oracle_topk.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+            L.cvs_oracle_scores.restype = ctypes.c_int
+            L.cvs_oracle_scores.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                            ctypes.c_int]
+            _lib = L
+    return _lib
+
+
+def _threads(threads):
+    return int(threads) if threads else (os.cpu_count() or 1)
+
+
+def _as_half(a) -> np.ndarray:
+    """fp16 numpy view of a numpy array or a torch tensor (any device)."""
+    if hasattr(a, "detach"):  # torch tensor
+        import torch
+
+        a = a.detach().to("cpu", torch.float16).contiguous().numpy()
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.float16:
+        a = a.astype(np.float16)
+    return a
+
+
+def topk(q, x, k: int, threads: int | None = None):
+    """Exact top-k of fp32(q . x) over fp16 inputs.  Returns (f32 [b,k], int64 [b,k]).
+
+    Restates ``reference.py:18-34`` with score-desc / id-asc order
+    (``kernels.cu:277-279``).
+    """
+    q16, x16 = _as_half(q), _as_half(x)
+    if q16.ndim == 1:
+        q16 = q16[None]
+    nq, d = q16.shape
+    n = x16.shape[0]
+    if x16.shape[1] != d:
+        raise ValueError("width mismatch")
+    k = int(k)
+    v = np.empty((nq, k), np.float32)
+    i = np.empty((nq, k), np.int64)
+    rc = lib().cvs_oracle_topk(q16.ctypes.data, x16.ctypes.data, nq, n, d, k,
+                               v.ctypes.data, i.ctypes.data, _threads(threads))
+    if rc != 0:
+        raise ValueError(f"oracle topk rejected nq={nq} n={n} d={d} k={k}")
+    return v, i
+
+
+def scores(q, x, threads: int | None = None) -> np.ndarray:
+    """fp32(q . x) for every pair (``kernels.cu:472-497``), exactly accumulated."""
+    q16, x16 = _as_half(q), _as_half(x)
+    nq, d = q16.shape
+    n = x16.shape[0]
+    out = np.empty((nq, n), np.float32)
+    rc = lib().cvs_oracle_scores(q16.ctypes.data, x16.ctypes.data, nq, n, d, out.ctypes.data,
+                                 _threads(threads))
+    if rc != 0:
+        raise ValueError("oracle scores rejected its arguments")
+    return out
+
+
+def _order(v: np.ndarray, ids: np.ndarray):
+    """Sort each row by (score desc, id asc)."""
+    sel = np.lexsort((ids, -v.astype(np.float64)), axis=-1)
+    return np.take_along_axis(v, sel, -1), np.take_along_axis(ids, sel, -1)
+
+
+def exact_topk_fp32(q, x, k: int, chunk: int = 1 << 18):
+    """numpy restatement of ``reference.py:18-34``: chunked fp32 matmul, running merge.
+
+    Ties are ordered by id so that the result is a function of its inputs.
+    """
+    qf = _as_half(q).astype(np.float32)
+    xh = _as_half(x)
+    best_v = best_i = None
+    for start in range(0, xh.shape[0], chunk):
+        s = qf @ xh[start:start + chunk].astype(np.float32).T
+        kk = min(k, s.shape[1])
+        ids = np.broadcast_to(np.arange(start, start + s.shape[1], dtype=np.int64), s.shape)
+        v, i = _order(s, ids)
+        v, i = v[:, :kk], i[:, :kk]
+        if best_v is not None:
+            v = np.concatenate([best_v, v], axis=1)
+            i = np.concatenate([best_i, i], axis=1)
+            v, i = _order(v, i)
+            v, i = v[:, :k], i[:, :k]
+        best_v, best_i = v, i
+    return best_v, best_i
+
+
+def torch_topk_cpu(q, x, k: int):
+    """The reference's CPU search path ``reference.py:8-15``: fp32 matmul + torch.topk."""
+    import torch
+
+    s = q @ x.T
+    v, i = torch.topk(s, k, dim=1)
+    return v.float(), i
+
+
+def numpy_search(q: np.ndarray, x: np.ndarray, k: int):
+    """``bench/bench_baselines.py:45-50``: matmul, argpartition, argsort of the k."""
+    s = q @ x.T
+    part = np.argpartition(-s, k - 1, axis=1)[:, :k]
+    pv = np.take_along_axis(s, part, 1)
+    order = np.argsort(-pv, axis=1)
+    return np.take_along_axis(pv, order, 1), np.take_along_axis(part, order, 1)
+
+
+class ParityError(AssertionError):
+    pass
+
+
+def check_exact(q, x, k: int, scores_got, ids_got, tol: float = 1e-3, full=None):
+    """Acceptance rule of ``tests/test_search.py:21-44`` plus id parity.
+
+    ``q``/``x`` are the prepared (normalised, unpadded) fp16 queries and stored
+    corpus.  Checks, against fp32 scores of the stored values:
+      * shape, id range, unique ids per row;
+      * every returned id scores at least the true k-th - tol*scale;
+      * returned scores match their ids' true scores within tol*scale;
+      * rows sorted (1e-6 slack, as the reference);
+      * id parity: every true top-k id whose score is above the k-th by more
+        than tol*scale is returned (so ids differ only inside the near-tie band).
+    Returns the exact-set recall (informational, as the reference).
+    """
+    v_got = np.asarray(scores_got.detach().cpu() if hasattr(scores_got, "detach") else scores_got,
+                       dtype=np.float32)
+    i_got = np.asarray(ids_got.detach().cpu() if hasattr(ids_got, "detach") else ids_got).astype(np.int64)
+    if full is None:
+        full = scores(q, x)
+    b, n = full.shape
+    if v_got.shape != (b, k) or i_got.shape != (b, k):
+        raise ParityError(f"shape {v_got.shape}/{i_got.shape} != {(b, k)}")
+    if (i_got < 0).any() or (i_got >= n).any():
+        raise ParityError("id out of range")
+    part = np.argpartition(-full, k - 1, axis=1)[:, :k]       # a true top-k (any tie order)
+    kth = np.take_along_axis(full, part, 1).min(axis=1, keepdims=True)
+    got_true = np.take_along_axis(full, i_got, 1)
+    scale = max(1.0, float(np.abs(full).max()))
+    band = tol * scale
+    if not (got_true >= kth - band).all():
+        raise ParityError("returned an id outside the true top-k")
+    if not (np.abs(v_got - got_true) <= band).all():
+        raise ParityError("scores do not match their ids")
+    if not (v_got[:, :-1] >= v_got[:, 1:] - 1e-6).all():
+        raise ParityError("results not sorted")
+    for row in i_got:
+        if len(set(row.tolist())) != k:
+            raise ParityError("duplicate ids")
+    for r in range(b):
+        must = np.nonzero(full[r] > kth[r, 0] + band)[0]
+        if not set(must.tolist()).issubset(set(i_got[r].tolist())):
+            raise ParityError(f"row {r}: a true top-k id outside the near-tie band is missing")
+    hit = sum(len(set(a) & set(c)) for a, c in zip(i_got.tolist(), part.tolist()))
+    return hit / i_got.size

@@ -1,0 +1,160 @@
+"""Pins the CPU oracle before anything is compared against it (CPU only).
+
+Each check is chosen so that a plausible oracle bug (wrong fp16 decoding, a
+dropped term, a wrong tie order, an off-by-one in the heap, transposed
+operands) fails at least one of them:
+
+* fp16 decoding: exhaustive over all 65536 bit patterns vs numpy.
+* golden vectors (tests/golden/*.npz): independent float64 brute force.
+* closed forms: k=1 is the arg-max (first index on ties), k=n is a full sort,
+  an identity corpus returns the query's own coordinates, duplicated rows tie
+  and are ordered by id, a transposed-operand score matrix is detected.
+* cross-checks against the numpy restatement of reference.py:18-34 and the
+  reference's CPU baselines (torch matmul+topk, numpy argpartition).
+* the acceptance rule (tests/test_search.py:21-44 + id parity) rejects planted
+  mistakes.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = sorted((Path(__file__).parent / "golden").glob("*.npz"))
+
+
+def unit(rng, m, d):
+    a = rng.standard_normal((m, d)).astype(np.float32)
+    return (a / np.linalg.norm(a, axis=1, keepdims=True)).astype(np.float16)
+
+
+def test_half_decoding_exhaustive():
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.cvs_oracle_half_to_float(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=[p.stem for p in GOLDEN])
+def test_oracle_matches_golden(path):
+    z = np.load(path)
+    k = int(z["k"])
+    v, i = oracle.topk(z["q"], z["x"], k)
+    np.testing.assert_allclose(v, z["scores"], rtol=0, atol=1e-6)
+    # ids identical except where two candidate scores are within 1e-6 (float64 vs
+    # double-accumulated-then-rounded scores may round differently there)
+    for r in range(v.shape[0]):
+        diff = np.nonzero(i[r] != z["ids"][r])[0]
+        for j in diff:
+            assert abs(float(z["scores"][r, j]) - float(v[r, j])) < 1e-6
+            near = np.abs(z["scores"][r] - z["scores"][r, j]) < 1e-6
+            assert near.sum() >= 2, f"{path.stem}: row {r} pos {j} differs without a tie"
+
+
+def test_golden_fixture_properties():
+    # the committed fixtures exercise what they claim to
+    names = {p.stem for p in GOLDEN}
+    assert {"k_one_n500_d128", "k_equals_n_n50_d64", "duplicates_n200_d32_k15",
+            "near_ties_n1000_d384_k100", "raw_ip_n400_d96_k20", "random_n300_d64_b5_k10"} <= names
+    z = np.load(GOLDEN[[p.stem for p in GOLDEN].index("duplicates_n200_d32_k15")])
+    s = z["scores"]
+    assert (s[:, :-1] == s[:, 1:]).any(), "duplicates fixture must contain exact ties"
+
+
+def test_k1_is_argmax():
+    rng = np.random.default_rng(1)
+    x, q = unit(rng, 777, 64), unit(rng, 9, 64)
+    full = q.astype(np.float64) @ x.astype(np.float64).T
+    v, i = oracle.topk(q, x, 1)
+    assert np.array_equal(i[:, 0], np.argmax(full, axis=1))
+
+
+def test_k_equals_n_is_full_sort():
+    rng = np.random.default_rng(2)
+    x, q = unit(rng, 64, 128), unit(rng, 4, 128)
+    full = q.astype(np.float64) @ x.astype(np.float64).T
+    v, i = oracle.topk(q, x, 64)
+    for r in range(4):
+        assert sorted(i[r].tolist()) == list(range(64))
+        assert np.all(np.diff(v[r]) <= 0)
+        np.testing.assert_array_equal(i[r], np.lexsort((np.arange(64), -full[r])))
+
+
+def test_identity_corpus_returns_query_coordinates():
+    rng = np.random.default_rng(3)
+    d = 64
+    x = np.eye(d, dtype=np.float16)
+    q = rng.standard_normal((5, d)).astype(np.float16)
+    v, i = oracle.topk(q, x, d)
+    for r in range(5):
+        np.testing.assert_array_equal(v[r], np.sort(q[r].astype(np.float32))[::-1])
+        np.testing.assert_array_equal(q[r, i[r]].astype(np.float32), v[r])
+
+
+def test_duplicates_tie_by_smaller_id():
+    rng = np.random.default_rng(4)
+    x = unit(rng, 50, 64)
+    x[[7, 19, 33]] = x[40]
+    q = x[40:41].copy()
+    v, i = oracle.topk(q, x, 4)
+    assert i[0].tolist() == [7, 19, 33, 40]
+    assert v[0, 0] == v[0, 1] == v[0, 2] == v[0, 3]
+
+
+def test_scores_not_transposed():
+    rng = np.random.default_rng(5)
+    x, q = unit(rng, 40, 64), unit(rng, 3, 64)
+    s = oracle.scores(q, x)
+    assert s.shape == (3, 40)
+    ref = q.astype(np.float64) @ x.astype(np.float64).T
+    np.testing.assert_allclose(s, ref, rtol=0, atol=1e-6)
+
+
+def test_restated_reference_and_cpu_baselines_agree():
+    rng = np.random.default_rng(6)
+    x, q = unit(rng, 5000, 384), unit(rng, 7, 384)
+    v, i = oracle.topk(q, x, 25)
+    ev, ei = oracle.exact_topk_fp32(q, x, 25, chunk=1024)
+    np.testing.assert_allclose(ev, v, atol=1e-5)
+    nv, ni = oracle.numpy_search(q.astype(np.float32), x.astype(np.float32), 25)
+    np.testing.assert_allclose(nv, v, atol=1e-5)
+    import torch
+
+    tv, ti = oracle.torch_topk_cpu(torch.from_numpy(q).float(), torch.from_numpy(x).float(), 25)
+    np.testing.assert_allclose(tv.numpy(), v, atol=1e-5)
+    for got in (ei, ni, ti.numpy()):
+        assert oracle.check_exact(q, x, 25, v, got) >= 0.99
+
+
+def test_check_exact_accepts_oracle_and_rejects_planted_mistakes():
+    rng = np.random.default_rng(7)
+    x, q = unit(rng, 3000, 128), unit(rng, 6, 128)
+    k = 20
+    v, i = oracle.topk(q, x, k)
+    assert oracle.check_exact(q, x, k, v, i) == 1.0
+
+    full = oracle.scores(q, x)
+    worst = np.argsort(full, axis=1)[:, :1]
+    bad = i.copy()
+    bad[:, 3] = worst[:, 0]
+    with pytest.raises(oracle.ParityError):
+        oracle.check_exact(q, x, k, v, bad)          # an id outside the top-k
+    with pytest.raises(oracle.ParityError):
+        oracle.check_exact(q, x, k, v + 0.01, i)     # scores off by 1e-2
+    with pytest.raises(oracle.ParityError):
+        oracle.check_exact(q, x, k, v[:, ::-1].copy(), i[:, ::-1].copy())  # unsorted
+    dup = i.copy()
+    dup[:, 1] = dup[:, 0]
+    dv = v.copy()
+    dv[:, 1] = dv[:, 0]
+    with pytest.raises(oracle.ParityError):
+        oracle.check_exact(q, x, k, dv, dup)         # duplicate ids
+    with pytest.raises(oracle.ParityError):
+        oracle.check_exact(q, x, k - 1, v[:, :k - 1], i[:, 1:])  # best id missing
