@@ -99,24 +99,30 @@ int check_inputs(const void* q, const void* x, int64_t nq, int64_t n, int64_t d)
 
 int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
 
-// Scan configuration for a query block of `bq` queries at width d (false if none).
+// Scan configuration for a query block of `bq` queries at width d (false if
+// none).  32x32x16 MFMA (full-rate on gfx950) whenever the queries of a wave
+// fit in VGPRs with it; 16x16x32 for bq = 16 and for rows wider than 768.
 bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
-  const int ks = ks_bucket(d);
   switch (bq) {
-    case 16: *c = {1, 1, 1, ks}; return true;
+    case 16:
+      *c = {16, 1, 1, 1, ks_bucket(d)};
+      return true;
     case 32:
-      if (d <= 768) { *c = {1, 2, 1, ks}; return true; }
-      *c = {2, 1, 1, 48};
+      if (d <= 384) { *c = {32, 1, 1, 1, 24}; return true; }
+      if (d <= 768) { *c = {32, 1, 1, 1, 48}; return true; }
+      *c = {16, 2, 1, 1, 48};
       return true;
     case 64:
-      if (d <= 384) { *c = {1, 4, 1, 12}; return true; }
-      *c = {4, 1, 2, ks};
+      if (d <= 384) { *c = {32, 1, 2, 1, 24}; return true; }
+      if (d <= 768) { *c = {32, 2, 1, 1, 48}; return true; }
+      *c = {16, 4, 1, 2, 48};
       return true;
     case 128:
-      if (d <= 768) { *c = {4, 2, 2, ks}; return true; }
+      if (d <= 384) { *c = {32, 4, 1, 2, 24}; return true; }
+      if (d <= 768) { *c = {32, 4, 1, 2, 48}; return true; }
       return false;
     case 256:
-      if (d <= 384) { *c = {4, 4, 4, 12}; return true; }
+      if (d <= 384) { *c = {32, 4, 2, 2, 24}; return true; }
       return false;
     default:
       return false;
@@ -217,8 +223,8 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     P.chunks = c;
     P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
     P.nlists = c * rs;
-    P.cap = std::max<int64_t>(128, pow2_at_least(k + 16 * P.cfg.rb));
-    const int64_t upt = 4 * rs;  // sampling units per tile
+    P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
+    const int64_t upt = P.cfg.units_per_tile();  // sampling units per tile
     const int64_t s = std::min<int64_t>(256, std::max<int64_t>(P.ntiles / 16, ceil_div(2 * k, upt)));
     P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
                 (((flags & CVS_FLAG_FORCE_PREPASS) && s <= P.ntiles) || (s >= 4 && s <= P.ntiles / 8));

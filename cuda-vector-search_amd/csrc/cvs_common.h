@@ -51,6 +51,41 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4));
 }
 
+// ---- HBM -> LDS DMA ---------------------------------------------------------
+
+// 16 bytes per lane from `src` into LDS at lds_base + 16*lane (one 1 KB block
+// per wave), bypassing VGPRs.  Issued through inline asm on purpose: the
+// compiler's own LDS-DMA tracking cannot tell the stage buffers apart and
+// would insert a full vmcnt(0) wait before every LDS read, serialising the
+// pipeline.  Callers therefore own all waits (wait_vmcnt* + s_barrier) before
+// reading a block.  `lds_base` must be wave-uniform.
+__device__ __forceinline__ void dma_to_lds_16(const void* src, const void* lds_block) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_block);
+  // m0 is restored afterwards: the compiler treats it as reserved.
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(base), "v"(src)
+      : "memory");
+}
+
+// ---- register placement -----------------------------------------------------
+
+// Returns `v` materialised in accumulation registers (AGPRs).  MFMA source
+// operands may live in AGPRs on gfx950, so long-lived MFMA inputs (the query
+// fragments) are pinned there, leaving the VGPRs to the streaming operands.
+// The asm emits no instruction; only the register-class constraint matters.
+__device__ __forceinline__ half8 pin_agpr(half8 v) {
+  half8 r = v;
+  asm volatile("" : "+a"(r));
+  return r;
+}
+
 // ---- wave utilities ---------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
@@ -119,6 +154,9 @@ __device__ __forceinline__ float wave_compact(float* lv, int* li, int count, int
   }
   const float kth = key_score(scratch[k - 1]);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Retire this rare path's own loads here, so the (hot) caller's loop does not
+  // inherit pending VGPR writes and wait on vmcnt(0) in every iteration.
+  wait_vmcnt<0>();
   return kth;
 }
 

@@ -78,14 +78,16 @@ struct SelectArgs {
   float* tau;          // [nq]    (threshold mode: score of the k-th best)
 };
 
-// Scan configurations (queries per wave QW = 16*QB; tile rows = RS*RB*16).
+// Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,
+// tile rows = rs*rb*ms, widest row = ksmax * (ms == 16 ? 32 : 16).
 struct ScanCfg {
-  int qs, qb, rb, ksmax;
-  int bq() const { return qs * 16 * qb; }
+  int ms, qs, qb, rb, ksmax;
+  int bq() const { return qs * ms * qb; }
   int rs() const { return 4 / qs; }
-  int tile_rows() const { return rs() * rb * 16; }
-  int wave_rows() const { return rb * 16; }
-  int dmax() const { return ksmax * 32; }
+  int tile_rows() const { return rs() * rb * ms; }
+  int wave_rows() const { return rb * ms; }
+  int dmax() const { return ksmax * (ms == 16 ? 32 : 16); }
+  int units_per_tile() const { return rs() * (64 / ms); }
 };
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).

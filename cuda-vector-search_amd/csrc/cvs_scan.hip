@@ -5,25 +5,34 @@
 // for gfx950:
 //
 //  * 256 threads = 4 wave64s, one per SIMD.  Queries are split QS ways across
-//    the waves and tile rows RS = 4/QS ways.  Each wave keeps its QW = 16*QB
+//    the waves and tile rows RS = 4/QS ways.  Each wave keeps its QW = MS*QB
 //    queries as MFMA B fragments in VGPRs for the whole launch (loaded once), so
 //    the corpus is the only operand that streams.
+//  * MFMA shape MS = 32 (v_mfma_f32_32x32x16_f16) wherever the query block
+//    allows it: on gfx950 it runs at the full dense fp16 rate, twice the
+//    throughput of v_mfma_f32_16x16x32_f16, which is kept (MS = 16) for batch
+//    <= 16 and for rows wider than 768.
 //  * Corpus rows stream HBM -> LDS with global_load_lds_dwordx4 (no VGPR
 //    staging), in 64-column stages.  Each 1 KB block of a stage is exactly one
-//    MFMA A fragment (16 rows x 32 columns) in lane order, so the ds_read_b128
-//    that feeds v_mfma_f32_16x16x32_f16 is contiguous and conflict free.
-//    NBUF stages are in flight (about 56 KB per CU); waits are explicit vmcnt
-//    counts because the compiler does not track LDS-DMA dependencies.
+//    MFMA A fragment in lane order, so the ds_read_b128 that feeds the MFMA is
+//    contiguous and conflict free.  NBUF stages are in flight (40-56 KB per
+//    CU); waits are explicit vmcnt counts.
 //  * Scores never leave VGPRs.  kAppend filters them against a per-query
-//    threshold and appends survivors to per-wave candidate lists (exact top-k
-//    is taken later by the select kernel); kMax records per-unit maxima for the
-//    sampling pre-pass that produces those thresholds; kStore* writes the full
+//    threshold (from the sampling pre-pass): a lane whose block maximum passes
+//    copies its whole row of scores to an LDS staging area (a few ds_writes,
+//    independent of how many scores pass); the staging area is flushed into
+//    per-wave candidate lists in global memory only when it fills and at the
+//    end, and that flush is where lists that overflow get compacted to their
+//    k best.  The exact top-k is taken later by the select kernel.  kMax
+//    records per-unit maxima for the sampling pre-pass; kStore* writes the full
 //    score matrix (Index.scores / twopass).
 //
-// MFMA layout used (v_mfma_f32_16x16x32_f16, A = 16x32 corpus rows, B = 32x16
-// queries): lane l supplies A[l%16][8*(l/16)..+7] and B[8*(l/16)..+7][l%16] and
-// receives D[4*(l/16)+i][l%16], i = 0..3.  Any consistent k-permutation of A
-// and B gives the same dot products, so only the D layout is load-bearing.
+// MFMA layouts (A = corpus rows, B = queries; any consistent k-permutation of
+// A and B gives the same dot products, so only the D layout is load-bearing):
+//   16x16x32: lane l supplies A[l%16][8(l/16)..+7], B[8(l/16)..+7][l%16] and
+//             receives D[4(l/16)+i][l%16], i = 0..3.
+//   32x32x16: lane l supplies A[l%32][8(l/32)..+7], B[8(l/32)..+7][l%32] and
+//             receives D[8i+4(l/32)+j][l%32], i, j = 0..3 (element 4i+j).
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 
@@ -31,33 +40,72 @@ namespace cvs {
 
 namespace {
 
-template <int QS, int QB, int RB, int KSMAX, int MODE>
+template <int MS>
+struct Mfma;
+
+template <>
+struct Mfma<16> {
+  typedef f32x4 acc_t;
+  static constexpr int KSZ = 32;  // k per instruction
+  static constexpr int NE = 4;    // accumulator elements per lane
+  __device__ static acc_t run(half8 a, half8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // row (within the 16-row block) of accumulator element e, minus 4*(lane/16)
+  __device__ static constexpr int row(int e) { return e; }
+};
+
+template <>
+struct Mfma<32> {
+  typedef float acc_t __attribute__((ext_vector_type(16)));
+  static constexpr int KSZ = 16;
+  static constexpr int NE = 16;
+  __device__ static acc_t run(half8 a, half8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // row (within the 32-row block) of element e = 4i+j, minus 4*(lane/32)
+  __device__ static constexpr int row(int e) { return 8 * (e >> 2) + (e & 3); }
+};
+
+template <int MS, int QS, int QB, int RB, int KSMAX, int MODE>
 __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
+  typedef Mfma<MS> M;
+  typedef typename M::acc_t acc_t;
   constexpr int RS = 4 / QS;
-  constexpr int QW = 16 * QB;
-  constexpr int BQ = QS * QW;
-  constexpr int TRB = RS * RB;      // 16-row blocks per tile
-  constexpr int TR = TRB * 16;      // tile rows
-  constexpr int FPS = TRB * 2;      // A fragments per 64-column stage
+  constexpr int QW = MS * QB;        // queries per wave
+  constexpr int BQ = QS * QW;        // queries per workgroup
+  constexpr int RW = MS * RB;        // rows per wave per tile
+  constexpr int TR = RS * RW;        // tile rows
+  constexpr int KPS = 64 / M::KSZ;   // MFMA k-steps per 64-column stage
+  constexpr int TRB = TR / MS;       // MS-row blocks per tile
+  constexpr int FPS = TRB * KPS;     // A fragments (1 KB each) per stage
   static_assert(FPS % 4 == 0, "every wave must issue the same number of stage loads");
-  constexpr int LPW = FPS / 4;      // stage loads per wave
+  constexpr int LPW = FPS / 4;       // stage loads per wave
   constexpr int STAGE = FPS * 1024;
-  constexpr int NBUF = (56 * 1024) / STAGE + 1;
-  static_assert((NBUF - 2) * LPW < 64, "vmcnt budget");
-  constexpr int NCMAX = KSMAX / 2;  // 64-column stages per tile (max)
+  constexpr int NBUF = ((QS == 4 ? 56 : 40) * 1024) / STAGE + 2;
+  static_assert((NBUF - 2) * LPW < 64 && NBUF >= 3, "vmcnt budget / pipeline depth");
+  constexpr int NCMAX = KSMAX / KPS; // 64-column stages per tile (max)
+  constexpr int G = kWave / MS;      // lane groups sharing a query column
+  constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
+  constexpr bool APP = (MODE == kAppend);
+  constexpr int STCAP = 64;          // staged lane-rows per wave
+  // Pin the query fragments to AGPRs when they dominate the register budget.
+  constexpr bool PIN_Q = QB * KSMAX * 4 >= 128;
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NBUF * STAGE];
-  __shared__ int lcnt[RS][BQ];
-  // Per-wave sort area for the (rare) list compaction; capacity <= kMaxCap.
-  __shared__ uint64_t sortbuf[MODE == kAppend ? 4 * kMaxCap : 1];
+  __shared__ int lcnt[RS][BQ];                        // entries in each owned list
+  __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
+  __shared__ float st_val[APP ? 4 : 1][APP ? NV : 1][STCAP];  // staged lane-rows, value-major
+  __shared__ int st_meta[APP ? 4 : 1][APP ? 2 * STCAP : 1];       // (query, first row)
+  __shared__ uint64_t sortbuf[APP ? 4 * kMaxCap : 1];  // compaction scratch
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int qs = w % QS;
   const int rs = w / QS;
-  const int c16 = lane & 15;
-  const int g = lane >> 4;
+  const int col = lane % MS;  // query column of this lane / A-fragment row
+  const int kg = lane / MS;   // k-group of this lane (0..G-1)
 
   // Workgroup -> (query group, chunk).  With xcd_pair, consecutive workgroups on
   // one XCD (ids i, i+8, ...) take the query groups of one chunk so that its
@@ -88,51 +136,40 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   const int64_t n = a.n;
   const int qwave0 = grp * BQ + qs * QW;
 
-  // Query fragments (B operand), resident for the whole launch.
-  half8 qf[QB][KSMAX];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qi = qwave0 + qb * 16 + c16;
-#pragma unroll
-    for (int ks = 0; ks < KSMAX; ++ks) {
-      half8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (qi < a.nq && ks * 32 < d) v = *(const half8*)(a.q + (int64_t)qi * d + ks * 32 + g * 8);
-      qf[qb][ks] = v;
-    }
-  }
-
-  float thr[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qi = qwave0 + qb * 16 + c16;
-    thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
-  }
-  if (MODE == kAppend) {
-    for (int i = tid; i < RS * BQ; i += kBlock) (&lcnt[0][0])[i] = 0;
-  }
-
   // Stage issue cursor (runs NBUF-1 stages ahead of the compute cursor).  Stages
   // past the end of this workgroup's range load a clamped, valid row so every
   // wave always has the same number of loads in flight.
   int64_t it_t = t_begin;
   int it_c = 0;
   int it_buf = 0;
+  // Per-lane source of each of this wave's stage loads (row, and the address
+  // of its first 64-column stage), advanced incrementally.
+  const _Float16* src[LPW];
+  int64_t src_row[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int f = w + 4 * j;
+    src_row[j] = t_begin * TR + (f % TRB) * MS + col;
+    src[j] = a.x + src_row[j] * d + (f / TRB) * M::KSZ + kg * 8;
+  }
   auto issue_next = [&]() {
     unsigned char* buf = smem + it_buf * STAGE;
+    const bool whole = (it_t + 1) * TR <= n;  // every row of this tile exists
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int f = w + 4 * j;
-      const int rbt = f % TRB;
-      const int kk = f / TRB;
-      int64_t row = it_t * TR + rbt * 16 + c16;
-      if (row >= n) row = n - 1;
-      const _Float16* src = a.x + row * d + it_c * 64 + kk * 32 + g * 8;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(buf + f * 1024),
-                                       16, 0, 0);
+      const _Float16* p = src[j] + it_c * 64;
+      if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * 64 + (f / TRB) * M::KSZ + kg * 8;
+      dma_to_lds_16(p, buf + f * 1024);
     }
     if (++it_c == nc) {
       it_c = 0;
       ++it_t;
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) {
+        src[j] += (int64_t)TR * d;
+        src_row[j] += TR;
+      }
     }
     if (++it_buf == NBUF) it_buf = 0;
   };
@@ -140,62 +177,176 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i) issue_next();
 
+  // Query fragments (B operand), resident for the whole launch.
+  half8 qf[QB][KSMAX];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = qwave0 + qb * MS + col;
+#pragma unroll
+    for (int ks = 0; ks < KSMAX; ++ks) {
+      half8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (qi < a.nq && ks * M::KSZ < d) v = *(const half8*)(a.q + (int64_t)qi * d + ks * M::KSZ + kg * 8);
+      qf[qb][ks] = PIN_Q ? pin_agpr(v) : v;
+    }
+  }
+
+  float thr[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = qwave0 + qb * MS + col;
+    thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+  }
+  if (APP) {
+    for (int i = tid; i < RS * BQ; i += kBlock) {
+      (&lcnt[0][0])[i] = 0;
+      const int qi = grp * BQ + i % BQ;
+      (&thr_s[0][0])[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+    }
+  }
+  int st_n = 0;  // wave-uniform count of staged lane-rows
+
+  // Appends the passing scores of this wave's staged lane-rows to its global
+  // candidate lists.  A list that fills up is compacted to its k best entries
+  // (raising that query's threshold) and the remaining scores are retried.
+  auto flush = [&]() {
+    const int list = chunk * RS + rs;
+#pragma unroll 1
+    for (int base = 0; base < st_n; base += kWave) {
+      const int er = base + lane;
+      const bool have = er < st_n;
+      const int ql = have ? st_meta[w][2 * er] : 0;
+      const int rbase = have ? st_meta[w][2 * er + 1] : 0;
+      const int ers = have ? er : 0;
+      const int64_t lbase = ((int64_t)(grp * BQ + ql) * a.nlists + list) * a.cap;
+      int next = have ? 0 : NV;  // first score of this lane-row not yet handled
+#pragma unroll 1
+      while (true) {
+        const float tq = thr_s[rs][ql];
+        int cnt = 0;
+#pragma unroll 1
+        for (int e = next; e < NV; ++e) cnt += (st_val[w][e][ers] >= tq) ? 1 : 0;
+        const int pos = cnt ? atomicAdd(&lcnt[rs][ql], cnt) : 0;
+        const int room = a.cap - pos;
+        int put = 0;
+        int e = next;
+#pragma unroll 1
+        for (; e < NV && put < room; ++e) {
+          const float v = st_val[w][e][ers];
+          if (v >= tq) {
+            a.lv[lbase + pos + put] = v;
+            a.li[lbase + pos + put] = rbase + (e / M::NE) * MS + M::row(e % M::NE);
+            ++put;
+          }
+        }
+        const bool over = put < cnt;
+        next = over ? e : NV;
+        uint64_t om = __ballot(over);
+        if (!om) break;
+#pragma unroll 1
+        while (om) {
+          const int ql0 = __shfl(ql, __ffsll((unsigned long long)om) - 1);
+          const int64_t base0 = ((int64_t)(grp * BQ + ql0) * a.nlists + list) * a.cap;
+          const float prev = thr_s[rs][ql0];
+          if (lane == 0) lcnt[rs][ql0] = a.cap;  // positions [0, cap) are all written
+          const float nt = fmaxf(prev, wave_compact(a.lv + base0, a.li + base0, a.cap, a.k,
+                                                    sortbuf + w * kMaxCap));
+          if (lane == 0) {
+            lcnt[rs][ql0] = a.k;
+            thr_s[rs][ql0] = nt;
+          }
+          om &= ~__ballot(ql == ql0);
+        }
+      }
+    }
+    st_n = 0;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
+  };
+
+  // Retire the query/threshold loads (and the prologue stages) before the loop:
+  // otherwise the compiler's wait-count analysis carries them around the loop
+  // back-edge and waits on vmcnt(0) at every stage.
+  wait_vmcnt<0>();
+
+  // A fragments of one stage (KPS k-steps x RB row blocks), read from LDS one
+  // stage ahead of the MFMAs that consume them.
+  auto read_stage = [&](int buf_idx, half8 (&f)[KPS][RB]) {
+    const unsigned char* buf = smem + buf_idx * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        f[kk][rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
+  };
+  half8 ab[2][KPS][RB];  // stage s in ab[s & 1] (static within a tile), stage s+1 prefetched
+  wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
+  __builtin_amdgcn_s_barrier();           // ... and for every wave
+  read_stage(0, ab[0]);
   int cur_buf = 0;
+
   for (int64_t t = t_begin; t < t_end; ++t) {
-    f32x4 acc[QB][RB];
+    acc_t acc[QB][RB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) acc[qb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < M::NE; ++e) acc[qb][rb][e] = 0.f;
 
 #pragma unroll
     for (int c = 0; c < NCMAX; ++c) {
       if (c < nc) {
-        // This wave's loads for the current stage have landed; the barrier makes
-        // every wave's loads visible and retires all reads of the buffer that
-        // issue_next() is about to overwrite.
-        wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();
+        // Stage s is in ab[c & 1].  Wait until stage s+1 has landed for every
+        // wave; the barrier also retires all reads of stage s-1's buffer, which
+        // issue_next() refills with stage s+NBUF-1.
+        wait_vmcnt_lgkm0<(NBUF - 3) * LPW>();
         __builtin_amdgcn_s_barrier();
         issue_next();
-        const unsigned char* buf = smem + cur_buf * STAGE;
+        const int nxt = (cur_buf + 1 == NBUF) ? 0 : cur_buf + 1;
+        read_stage(nxt, ab[(c + 1) & 1]);
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          half8 af[RB];
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-            af[rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
+        for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
-              acc[qb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rb], qf[qb][2 * c + kk],
-                                                                   acc[qb][rb], 0, 0, 0);
-        }
-        if (++cur_buf == NBUF) cur_buf = 0;
+              acc[qb][rb] = M::run(ab[c & 1][kk][rb], qf[qb][KPS * c + kk], acc[qb][rb]);
+        cur_buf = nxt;
       }
     }
+    if (nc & 1) {  // the next tile's first stage sits in ab[1]
+#pragma unroll
+      for (int kk = 0; kk < KPS; ++kk)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) ab[0][kk][rb] = ab[1][kk][rb];
+    }
 
-    // ---- epilogue: acc[qb][rb][i] = score(query qwave0+16qb+c16, row rowb+16rb+i)
-    const int64_t rowb = t * TR + (rs * RB) * 16 + g * 4;
+    // ---- epilogue: acc[qb][rb][e] = score(query qwave0 + MS*qb + col,
+    //                                        row rowb + MS*rb + M::row(e))
+    const int64_t rowb = t * TR + rs * RW + 4 * kg;
     const bool partial = (t * TR + TR > n);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const int qi = qwave0 + qb * 16 + c16;
-      float v[RB * 4];
+      const int qi = qwave0 + qb * MS + col;
+      float v[NV];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float s = acc[qb][rb][i];
-          if (partial && rowb + rb * 16 + i >= n) s = -__builtin_inff();
-          v[rb * 4 + i] = s;
-        }
+        for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = acc[qb][rb][e];
+      if (partial) {  // only the corpus's last tile has rows past n
+        const int64_t left = n - rowb;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int e = 0; e < M::NE; ++e)
+            if (rb * MS + M::row(e) >= left) v[rb * M::NE + e] = -__builtin_inff();
+      }
 
       if (MODE == kStoreF32 || MODE == kStoreF16) {
         if (qi < a.nq) {
 #pragma unroll
-          for (int j = 0; j < RB * 4; ++j) {
-            const int64_t row = rowb + (j / 4) * 16 + (j % 4);
+          for (int j = 0; j < NV; ++j) {
+            const int64_t row = rowb + (j / M::NE) * MS + M::row(j % M::NE);
             if (row < n) {
               if (MODE == kStoreF32)
                 ((float*)a.out)[(int64_t)qi * n + row] = v[j];
@@ -204,62 +355,39 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
             }
           }
         }
-      } else if (MODE == kMax) {
+      } else {
         float m = v[0];
 #pragma unroll
-        for (int j = 1; j < RB * 4; ++j) m = fmaxf(m, v[j]);
-        if (qi < a.nq) a.umax[(int64_t)qi * a.units + chunk * (RS * 4) + rs * 4 + g] = m;
-      } else {  // kAppend
-        float m = v[0];
-#pragma unroll
-        for (int j = 1; j < RB * 4; ++j) m = fmaxf(m, v[j]);
-        if (__ballot(m >= thr[qb]) != 0ull) {
-          const int ql = qs * QW + qb * 16 + c16;
-          const int list = chunk * RS + rs;
-          int my = 0;
-#pragma unroll
-          for (int j = 0; j < RB * 4; ++j) my += (v[j] >= thr[qb]) ? 1 : 0;
-          int tot = my + __shfl_xor(my, 16);
-          tot += __shfl_xor(tot, 32);
-          const bool need = (qi < a.nq) && (lcnt[rs][ql] + tot > a.cap);
-          uint64_t needm = __ballot(need);
-          while (needm) {
-            const int cq = (__ffsll((unsigned long long)needm) - 1) & 15;
-            const int ql0 = qs * QW + qb * 16 + cq;
-            const int64_t base0 = ((int64_t)(grp * BQ + ql0) * a.nlists + list) * a.cap;
-            const int count0 = lcnt[rs][ql0];
-            const float nt = wave_compact(a.lv + base0, a.li + base0, count0, a.k, sortbuf + w * kMaxCap);
-            if (lane == 0) lcnt[rs][ql0] = a.k;
-            if (c16 == cq) thr[qb] = fmaxf(thr[qb], nt);
-            needm &= ~(0x0001000100010001ull << cq);
-          }
-          my = 0;
-#pragma unroll
-          for (int j = 0; j < RB * 4; ++j) my += (v[j] >= thr[qb]) ? 1 : 0;
-          if (my > 0 && qi < a.nq) {
-            int pos = atomicAdd(&lcnt[rs][ql], my);
-            const int64_t base = ((int64_t)qi * a.nlists + list) * a.cap;
-            float* lv = a.lv + base;
-            int* li = a.li + base;
-#pragma unroll
-            for (int j = 0; j < RB * 4; ++j) {
-              if (v[j] >= thr[qb]) {
-                lv[pos] = v[j];
-                li[pos] = (int)(rowb + (j / 4) * 16 + (j % 4));
-                ++pos;
-              }
+        for (int j = 1; j < NV; ++j) m = fmaxf(m, v[j]);
+        if (MODE == kMax) {
+          if (qi < a.nq) a.umax[(int64_t)qi * a.units + chunk * (RS * G) + rs * G + kg] = m;
+        } else {  // kAppend
+          uint64_t mk = __ballot(m >= thr[qb]);
+          if (mk) {
+            if (st_n + __popcll(mk) > STCAP) {
+              flush();
+              mk = __ballot(m >= thr[qb]);
             }
+            if (m >= thr[qb]) {
+              const int p = st_n + lanes_below(mk);
+#pragma unroll
+              for (int j = 0; j < NV; ++j) st_val[w][j][p] = v[j];
+              st_meta[w][2 * p] = qs * QW + qb * MS + col;
+              st_meta[w][2 * p + 1] = (int)rowb;
+            }
+            st_n += __popcll(mk);
           }
         }
       }
     }
   }
+  if (APP && st_n > 0) flush();
 
   // Drain the trailing (dummy) stage loads before this workgroup's LDS can be
   // handed to another one, and make all list counts final.
   wait_vmcnt_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
-  if (MODE == kAppend) {
+  if (APP) {
     for (int i = tid; i < RS * BQ; i += kBlock) {
       const int r = i / BQ;
       const int ql = i % BQ;
@@ -269,24 +397,20 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   }
 }
 
-struct CfgKey {
-  int qs, qb, rb, ksmax;
-};
-
-template <int QS, int QB, int RB, int KS>
+template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   switch (mode) {
     case kAppend:
-      hipLaunchKernelGGL((scan_kernel<QS, QB, RB, KS, kAppend>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kMax:
-      hipLaunchKernelGGL((scan_kernel<QS, QB, RB, KS, kMax>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kStoreF32:
-      hipLaunchKernelGGL((scan_kernel<QS, QB, RB, KS, kStoreF32>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kStoreF16:
-      hipLaunchKernelGGL((scan_kernel<QS, QB, RB, KS, kStoreF16>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;
@@ -294,35 +418,37 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The instantiated configurations: (QS, QB, RB, KSMAX).
+// The instantiated configurations: (MS, QS, QB, RB, KSMAX).  KSMAX * KSZ is the
+// widest row each one accepts (KSZ = 32 for MS = 16, 16 for MS = 32).
 #define CVS_SCAN_CONFIGS(X) \
-  X(1, 1, 1, 12)            \
-  X(1, 1, 1, 24)            \
-  X(1, 1, 1, 48)            \
-  X(1, 2, 1, 12)            \
-  X(1, 2, 1, 24)            \
-  X(2, 1, 1, 48)            \
-  X(1, 4, 1, 12)            \
-  X(4, 1, 2, 24)            \
-  X(4, 1, 2, 48)            \
-  X(4, 2, 2, 12)            \
-  X(4, 2, 2, 24)            \
-  X(4, 4, 4, 12)
+  X(16, 1, 1, 1, 12)        \
+  X(16, 1, 1, 1, 24)        \
+  X(16, 1, 1, 1, 48)        \
+  X(16, 2, 1, 1, 48)        \
+  X(16, 4, 1, 2, 48)        \
+  X(32, 1, 1, 1, 24)        \
+  X(32, 1, 1, 1, 48)        \
+  X(32, 1, 2, 1, 24)        \
+  X(32, 2, 1, 1, 48)        \
+  X(32, 4, 1, 2, 24)        \
+  X(32, 4, 1, 2, 48)        \
+  X(32, 4, 2, 2, 24)
 
 }  // namespace
 
 bool scan_cfg_available(const ScanCfg& c, int mode) {
   if (mode < kAppend || mode > kStoreF16) return false;
-#define CVS_HAS(QS, QB, RB, KS) \
-  if (c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return true;
+#define CVS_HAS(MS, QS, QB, RB, KS) \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return true;
   CVS_SCAN_CONFIGS(CVS_HAS)
 #undef CVS_HAS
   return false;
 }
 
 hipError_t launch_scan(const ScanCfg& c, int mode, const ScanArgs& a, int grid, hipStream_t s) {
-#define CVS_LAUNCH(QS, QB, RB, KS) \
-  if (c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return launch_one<QS, QB, RB, KS>(mode, a, grid, s);
+#define CVS_LAUNCH(MS, QS, QB, RB, KS)                                              \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) \
+    return launch_one<MS, QS, QB, RB, KS>(mode, a, grid, s);
   CVS_SCAN_CONFIGS(CVS_LAUNCH)
 #undef CVS_LAUNCH
   return hipErrorInvalidValue;

@@ -2,11 +2,14 @@
 //
 // Replaces the merge of csrc/kernels.cu:373-445.  The reference merges exactly
 // k candidates per chunk with one warp and k serial arg-max rounds; here each
-// query's candidates (any number per list) are streamed in batches of 1024,
-// filtered against the running k-th best key, and the survivors are sorted in
-// LDS with a block-wide bitonic network whenever the buffer could overflow.
-// Keys order by (score desc, id asc) and are unique, so the k largest keys are
-// exactly the top-k and the output comes out sorted like the reference's.
+// query's candidates (any number per list) are streamed into an LDS buffer in
+// batches, filtered against the running k-th best key, and the buffer is cut
+// down to its k best keys with a radix select (8-bit digits of the 64-bit key,
+// most significant first, per-wave LDS histograms, early exit once the k-th
+// key's digit bin is exhausted) followed by one compaction pass.  Only the
+// final k survivors are sorted.  Keys order by (score desc, id asc) and are
+// unique, so the k largest keys are exactly the top-k and the output is sorted
+// like the reference's.
 //
 // Threshold mode returns only the score of the k-th best key (used to turn the
 // sampling pre-pass's unit maxima into per-query thresholds).
@@ -17,9 +20,92 @@ namespace cvs {
 
 namespace {
 
-constexpr int kBuf = 2048;
-constexpr int kBatch = 1024;
+constexpr int kBuf = 4096;    // LDS key buffer
+constexpr int kBatch = 2048;  // candidates gathered per round
+constexpr int kWaves = kBlock / kWave;
 
+struct SelShared {
+  uint64_t keys[kBuf];
+  int pre[kSelectMaxLists + 1];
+  int part[kBlock];
+  int hist[kWaves][256];
+  int nbuf;
+  int ncut;
+  int digit;
+  int above;
+  int stop;
+  uint64_t thr_key;
+};
+
+// Cuts keys[0..nb) down to its k largest keys (nb > k), in place and in any
+// order, and returns the k-th largest key.  Whole block.
+__device__ uint64_t block_keep_top(SelShared& S, int nb, int k) {
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  const int lane = tid % kWave;
+  uint64_t prefix = 0, pmask = 0;
+  int need = k;  // rank of the wanted key among keys matching `prefix`
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = tid; i < kWaves * 256; i += kBlock) (&S.hist[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < nb; i += kBlock) {
+      const uint64_t key = S.keys[i];
+      if ((key & pmask) == prefix) atomicAdd(&S.hist[w][(int)((key >> shift) & 255)], 1);
+    }
+    __syncthreads();
+    // digit d such that (#keys with digit > d) < need <= (#keys with digit >= d)
+    if (w == 0) {
+      int c[4];
+      int s = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
+        const int b = 255 - (4 * lane + j);
+        c[j] = S.hist[0][b] + S.hist[1][b] + S.hist[2][b] + S.hist[3][b];
+        s += c[j];
+      }
+      // exclusive prefix over lanes of s (descending bin order)
+      int incl = s;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+      }
+      int run = incl - s;  // keys in bins strictly above this lane's first bin
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (run < need && need <= run + c[j]) {
+          S.digit = 255 - (4 * lane + j);
+          S.above = run;
+          S.stop = (run + c[j] == need) ? 1 : 0;
+        }
+        run += c[j];
+      }
+    }
+    __syncthreads();
+    const uint64_t dg = (uint64_t)S.digit;
+    need -= S.above;
+    prefix |= dg << shift;
+    pmask |= 255ull << shift;
+    if (S.stop) break;  // every key with this prefix is in the top k
+    __syncthreads();
+  }
+  // keep keys >= prefix (with the undecided low bits at zero): exactly k keys
+  if (tid == 0) S.ncut = 0;
+  __syncthreads();
+  uint64_t keep[kBuf / kBlock];
+  int nk = 0;
+  for (int i = tid; i < nb; i += kBlock) {
+    const uint64_t key = S.keys[i];
+    if (key >= prefix) keep[nk++] = key;
+  }
+  __syncthreads();
+  int pos = nk ? atomicAdd(&S.ncut, nk) : 0;
+  for (int j = 0; j < nk; ++j) S.keys[pos + j] = keep[j];
+  __syncthreads();
+  return prefix;
+}
+
+// Descending bitonic sort of keys[0..N) (N a power of two), whole block.
 __device__ void block_sort_desc(uint64_t* keys, int N) {
   const int tid = threadIdx.x;
   for (int size = 2; size <= N; size <<= 1) {
@@ -41,12 +127,7 @@ __device__ void block_sort_desc(uint64_t* keys, int N) {
 
 template <int TAU_MODE>
 __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
-  __shared__ uint64_t keys[kBuf];
-  __shared__ int pre[kSelectMaxLists + 1];
-  __shared__ int part[kBlock];
-  __shared__ int nbuf;
-  __shared__ uint64_t thr_key;
-
+  __shared__ SelShared S;
   const int tid = threadIdx.x;
   const int q = blockIdx.x;
   const int NL = a.nlists;
@@ -58,77 +139,94 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int l1 = min(NL, l0 + per);
   int sum = 0;
   for (int L = l0; L < l1; ++L) sum += a.lcount ? a.lcount[(int64_t)q * NL + L] : a.cap;
-  part[tid] = sum;
+  S.part[tid] = sum;
   if (tid == 0) {
-    nbuf = 0;
-    thr_key = 0ull;
+    S.nbuf = 0;
+    S.thr_key = 0ull;
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int i = 0; i < kBlock; ++i) {
-      const int v = part[i];
-      part[i] = run;
-      run += v;
+  if (tid < kWave) {  // scan of the 256 partial sums by wave 0
+    int v[4], s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = S.part[4 * tid + j];
+      s += v[j];
     }
-    pre[NL] = run;
+    int incl = s;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int o = __shfl_up(incl, off);
+      if (tid >= off) incl += o;
+    }
+    int run = incl - s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      S.part[4 * tid + j] = run;
+      run += v[j];
+    }
+    if (tid == kWave - 1) S.pre[NL] = incl;
   }
   __syncthreads();
   {
-    int run = part[tid];
+    int run = S.part[tid];
     for (int L = l0; L < l1; ++L) {
-      pre[L] = run;
+      S.pre[L] = run;
       run += a.lcount ? a.lcount[(int64_t)q * NL + L] : a.cap;
     }
   }
   __syncthreads();
-  const int total = pre[NL];
+  const int total = S.pre[NL];
 
   for (int base = 0; base < total; base += kBatch) {
-    const uint64_t t = thr_key;
+    const uint64_t t = S.thr_key;
     for (int j = 0; j < kBatch / kBlock; ++j) {
       const int gi = base + j * kBlock + tid;
       if (gi < total) {
-        // largest L with pre[L] <= gi
-        int lo = 0, hi = NL;
+        int lo = 0, hi = NL;  // largest L with pre[L] <= gi
         while (hi - lo > 1) {
           const int mid = (lo + hi) >> 1;
-          if (pre[mid] <= gi) lo = mid; else hi = mid;
+          if (S.pre[mid] <= gi) lo = mid; else hi = mid;
         }
-        const int idx = gi - pre[lo];
+        const int idx = gi - S.pre[lo];
         const int64_t off = ((int64_t)q * NL + lo) * a.cap + idx;
         const int id = a.li ? a.li[off] : (int)((int64_t)lo * a.cap + idx);
         const uint64_t key = make_key(a.lv[off], id);
-        if (key > t) keys[atomicAdd(&nbuf, 1)] = key;
+        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
       }
     }
     __syncthreads();
-    const int nb = nbuf;
+    const int nb = S.nbuf;
     const bool last = base + kBatch >= total;
-    if (nb > kBuf - kBatch || (last && nb > 0)) {
-      int N = 2;
-      while (N < nb) N <<= 1;
-      for (int i = nb + tid; i < N; i += kBlock) keys[i] = 0ull;
-      __syncthreads();
-      block_sort_desc(keys, N);
+    if (nb > kBuf - kBatch || (last && nb > k)) {
+      const uint64_t kth = block_keep_top(S, nb, k);
       if (tid == 0) {
-        if (nb >= k) {
-          nbuf = k;
-          thr_key = keys[k - 1];
-        }
+        S.nbuf = k;
+        S.thr_key = kth;
       }
       __syncthreads();
     }
   }
 
-  const int nb = min(nbuf, k);
+  const int nb = min(S.nbuf, k);
   if (TAU_MODE) {
-    if (tid == 0) a.tau[q] = (nb >= k) ? key_score(keys[k - 1]) : -__builtin_inff();
+    // the k-th best key is the smallest survivor
+    if (tid < kWave) {
+      uint64_t m = ~0ull;
+      for (int i = tid; i < nb; i += kWave) m = min(m, S.keys[i]);
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
+      if (tid == 0) a.tau[q] = (nb >= k) ? key_score(m) : -__builtin_inff();
+    }
   } else {
+    int N = 2;
+    while (N < nb) N <<= 1;
+    for (int i = nb + tid; i < N; i += kBlock) S.keys[i] = 0ull;
+    __syncthreads();
+    block_sort_desc(S.keys, N);
     for (int r = tid; r < k; r += kBlock) {
       const bool ok = r < nb;
-      a.out_v[(int64_t)q * k + r] = ok ? key_score(keys[r]) : -__builtin_inff();
-      a.out_i[(int64_t)q * k + r] = ok ? key_id(keys[r]) : -1;
+      a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
+      a.out_i[(int64_t)q * k + r] = ok ? key_id(S.keys[r]) : -1;
     }
   }
 }
