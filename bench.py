@@ -12,9 +12,13 @@ config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
 * value / ms_per_step: host-timed whole-batch throughput (queries/s) over K steps
   bracketed by device synchronisation;
 * roofline: the dominant kernel (the MFMA scan, or the GEMV at batch 1) timed
-  with HIP events on the stream it runs on, against its algorithmic bytes
+  with HIP events that the library records on the stream it launches on, over
+  a second timed region of K back-to-back calls, against its algorithmic bytes
   (corpus read once + queries) and the MI355X peaks (8 TB/s HBM; 2.5 PFLOP/s
-  dense fp16 MFMA also reported as mfma_frac);
+  dense fp16 MFMA also reported as mfma_frac).  ``traffic`` is the kernel's
+  measured HBM bytes per launch: two child runs of this script under
+  ``rocprofv3 --pmc`` (FETCH_SIZE, then WRITE_SIZE), each scaled by what the
+  same counter reads for a plain 1 GiB device copy in the same child;
 * cpu_baseline: the reference's CPU search path (fp32 torch matmul + topk,
   reference.py:8-15) and the numpy baseline (bench/bench_baselines.py:45-50),
   both as restated in oracle/, timed on this host on a bounded sample of the
@@ -26,6 +30,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -78,13 +83,16 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
     dev_ms = e0.elapsed_time(e1) / steps
 
-    # per-stage device time on the engine's stream (HIP events inside the library)
+    # Second timed region: the same K calls back to back, with the library
+    # recording HIP events between its launches on the stream it uses.
     qq = index._prep_queries(q)
-    stage = []
-    for _ in range(max(5, min(20, steps))):
-        (_, _, plan), ms = eng.fused_topk_timed(qq, index._x, k)
-        stage.append(ms)
-    stage_ms = [statistics.median(s[i] for s in stage) for i in range(4)]
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        _, _, plan = eng.fused_topk_marked(qq, index._x, k, marks[i])
+    torch.cuda.synchronize()
+    per_step = [[m[j].elapsed_time(m[j + 1]) for j in range(4)] for m in marks]
+    stage_ms = [statistics.fmean(s[j] for s in per_step) for j in range(4)]
     kern_ms = stage_ms[2]
     nbytes = kernel_bytes(n, index._x.shape[1], b)
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
@@ -103,6 +111,89 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
     }
     log(f"[{name}] {json.dumps(row)}")
     return row, (index, q, k, out)
+
+
+# Demangled names of the dominant kernel's dispatches (mode 0 = candidate append).
+DOMINANT = {"scan": re.compile(r"scan_kernel<[^>]*,\s*0>"), "gemv": re.compile(r"gemv_kernel<\d+,\s*0>")}
+COPY_KERNEL = re.compile(r"copyBuffer")  # torch copy_ between device tensors = hipMemcpyAsync
+COPY_BYTES = 1 << 30
+
+
+def pmc_child(name):
+    """Body of one ``rocprofv3 --pmc`` child: a few searches of config `name`,
+    then a plain device copy of COPY_BYTES for the counter's calibration."""
+    import torch
+
+    from cuda_vector_search import Index, synthetic
+
+    n, d, b, k, ties = synthetic.CONFIGS[name]
+    x = synthetic.unit_corpus(n, d, seed=d, device="cuda")
+    if ties:
+        synthetic.inject_near_ties(x, seed=7)
+    q = synthetic.unit_queries(b, d, seed=1, device="cuda")
+    index = Index(x, metric="ip", copy=False)
+    for _ in range(3):
+        index.search(q, k)
+    torch.cuda.synchronize()
+    del index, x
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"pmc child {name}: 3 searches, 3 copies of {COPY_BYTES} bytes", flush=True)
+
+
+def measure_traffic(name, batch):
+    """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc child
+    runs; None (with the reason) when rocprofv3 is absent or a run fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not on PATH"
+    pat = DOMINANT["gemv" if batch == 1 else "scan"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out_dir = tempfile.mkdtemp(prefix=f"cvs_pmc_{counter}_", dir="/tmp")
+        cmd = ["timeout", "-k", "10", "-s", "KILL", "240", "rocprofv3", "--pmc", counter, "-f", "csv",
+               "-d", out_dir, "-o", "pmc", "--", sys.executable, str(REPO / "bench.py"),
+               "--pmc-child", name]
+        log(f"[traffic] rocprofv3 --pmc {counter} child run ...")
+        t0 = time.perf_counter()
+        r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                           text=True)
+        log(f"[traffic] {counter}: exit {r.returncode} after {time.perf_counter() - t0:.1f} s")
+        files = sorted(Path(out_dir).rglob("*counter_collection.csv"))
+        if r.returncode != 0 or not files:
+            tail = "\n".join(r.stdout.splitlines()[-5:])
+            shutil.rmtree(out_dir, ignore_errors=True)
+            return None, f"rocprofv3 --pmc {counter} failed (exit {r.returncode}): {tail}"
+        kern, copy = [], []
+        for f in files:
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if row.get("Counter_Name") != counter:
+                        continue
+                    kname = row.get("Kernel_Name", "")
+                    if pat.search(kname):
+                        kern.append(float(row["Counter_Value"]))
+                    elif COPY_KERNEL.search(kname):
+                        copy.append(float(row["Counter_Value"]))
+        shutil.rmtree(out_dir, ignore_errors=True)
+        # the calibration copies are the child's largest (corpus set-up copies less)
+        big_copies = [c for c in copy if copy and c >= 0.75 * max(copy)]
+        if not kern or not big_copies:
+            return None, f"{counter}: no dispatches matched (kernel {len(kern)}, copy {len(big_copies)})"
+        scale = COPY_BYTES / (statistics.median(big_copies) * 1024.0)
+        res[counter] = {"kib_per_launch": statistics.median(kern), "copy_kib": statistics.median(big_copies),
+                        "scale": round(scale, 4)}
+    traffic = sum(v["kib_per_launch"] * 1024.0 * v["scale"] for v in res.values())
+    return int(round(traffic)), res
 
 
 def cpu_baseline(index, q, k, gpu_ids, torch, sample_q=32, target_s=10.0):
@@ -159,7 +250,13 @@ def main():
                     help="first entry is the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
+    ap.add_argument("--pmc-child", metavar="CONFIG", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_child:
+        pmc_child(args.pmc_child)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -167,6 +264,15 @@ def main():
               "the exact top-k engine is a single-GPU build; multi-GPU sharding is design-only.",
               file=sys.stderr, flush=True)
         sys.exit(2)
+
+    names = [c.strip() for c in args.configs.split(",") if c.strip()]
+    # Counter runs first, in child processes, before this process touches the GPU.
+    traffic, traffic_detail = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:
+        from cuda_vector_search.synthetic import CONFIGS
+
+        traffic, traffic_detail = measure_traffic(names[0], CONFIGS[names[0]][2])
+        log(f"[traffic] {traffic} bytes/launch: {traffic_detail}")
 
     import torch
 
@@ -176,7 +282,6 @@ def main():
         print("bench.py needs an AMD Instinct MI355X (gfx950) GPU", file=sys.stderr)
         sys.exit(1)
     eng = _ext.load()
-    names = [c.strip() for c in args.configs.split(",") if c.strip()]
 
     rows = []
     head = None
@@ -224,7 +329,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": row["kernel_hbm_frac"],
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_detail": traffic_detail,
             "kernel_ms": kern_ms,
             "algorithmic_bytes": kernel_bytes(n, d, b),
             "mfma_frac": row["kernel_mfma_frac"],

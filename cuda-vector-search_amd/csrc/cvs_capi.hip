@@ -470,6 +470,20 @@ int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, in
   return rc;
 }
 
+int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                          int64_t bq, int64_t chunks, int flags, void* workspace,
+                          int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                          int device, void* stream, void* const* marks) {
+  if (marks == nullptr) return fail(CVS_ERR_INVALID, "marks must not be null");
+  hipEvent_t ev[5];
+  for (int i = 0; i < 5; ++i) {
+    if (marks[i] == nullptr) return fail(CVS_ERR_INVALID, "marks[%d] is null", i);
+    ev[i] = reinterpret_cast<hipEvent_t>(marks[i]);
+  }
+  return run_fused(q, x, nq, n, d, k, bq, chunks, flags, workspace, workspace_bytes, out_v, out_i,
+                   plan_out, device, stream, nq > 0 ? ev : nullptr);
+}
+
 int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, void* out, int out_fp32,
                int device, void* stream) {
   DevInfo di;

@@ -65,6 +65,10 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.cvs_fused_topk_timed.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                          vp, vp, ctypes.POINTER(i64), i32, vp,
                                          ctypes.POINTER(ctypes.c_float)]
+    lib.cvs_fused_topk_marked.restype = i32
+    lib.cvs_fused_topk_marked.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
+                                          vp, vp, ctypes.POINTER(i64), i32, vp,
+                                          ctypes.POINTER(vp)]
     return lib
 
 
@@ -156,7 +160,19 @@ class Engine:
         out = self._fused(q, x, k, bq, chunks, flags, ms)
         return out, [float(v) for v in ms]
 
-    def _fused(self, q, x, k, bq, chunks, flags, stage_ms):
+    def fused_topk_marked(self, q, x, k: int, marks, bq: int = 0, chunks: int = 0, flags: int = 0):
+        """fused_topk that records the five timing-enabled ``torch.cuda.Event``s in
+        ``marks`` around its four stages on the current stream, without blocking
+        (read them with ``marks[i].elapsed_time(marks[i + 1])`` after a sync)."""
+        if len(marks) != 5:
+            raise ValueError("marks must hold 5 events")
+        for ev in marks:
+            if not ev.cuda_event:  # torch creates the HIP event at its first record
+                ev.record()
+        handles = (ctypes.c_void_p * 5)(*[ev.cuda_event for ev in marks])
+        return self._fused(q, x, k, bq, chunks, flags, None, handles)
+
+    def _fused(self, q, x, k, bq, chunks, flags, stage_ms, marks=None):
         import torch
 
         self._check_pair(q, x)
@@ -178,7 +194,9 @@ class Engine:
         ws = torch.empty(max(int(ws_bytes.value), 256), dtype=torch.uint8, device=dev)
         args = (q.data_ptr(), x.data_ptr(), nq, n, d, k, bq, chunks, flags, ws.data_ptr(), ws.numel(),
                 out_v.data_ptr(), out_i.data_ptr(), plan_c, dev.index, self._stream(dev))
-        if stage_ms is None:
+        if marks is not None:
+            rc = self.lib.cvs_fused_topk_marked(*args, marks)
+        elif stage_ms is None:
             rc = self.lib.cvs_fused_topk(*args)
         else:
             rc = self.lib.cvs_fused_topk_timed(*args, stage_ms)

@@ -106,6 +106,19 @@ int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, in
                          int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
                          int device, void* stream, float* stage_ms);
 
+/*
+ * Non-blocking diagnostic twin of cvs_fused_topk (no counterpart in the
+ * reference): runs the same launches and records the caller's five HIP events
+ * marks[0..4] (hipEvent_t handles, created by the caller with timing enabled)
+ * on `stream` around the four pipeline stages, in the order of
+ * cvs_fused_topk_timed.  Returns without waiting, so a benchmark can time many
+ * back-to-back calls and read the events afterwards.
+ */
+int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                          int64_t bq, int64_t chunks, int flags, void* workspace,
+                          int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                          int device, void* stream, void* const* marks);
+
 #ifdef __cplusplus
 }
 #endif

@@ -249,6 +249,25 @@ def test_prepass_does_not_change_results(eng, flags, n, d, b, k):
     np.testing.assert_array_equal(i, i0)
 
 
+@pytest.mark.parametrize("n,d,b,k", [(50000, 384, 256, 10), (70000, 768, 1, 10)])
+def test_timed_and_marked_twins_match(eng, n, d, b, k):
+    """The diagnostic entry points run the same launches as fused_topk: identical
+    outputs, and stage times that account for the work (scan/GEMV > 0)."""
+    say(f"timed/marked twins n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=5)
+    qd, xd = q.cuda(), x.cuda()
+    v0, i0, p0 = eng.fused_topk(qd, xd, k)
+    (v1, i1, p1), ms = eng.fused_topk_timed(qd, xd, k)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    v2, i2, p2 = eng.fused_topk_marked(qd, xd, k, marks)
+    torch.cuda.synchronize()
+    for v, i, p in ((v1, i1, p1), (v2, i2, p2)):
+        assert torch.equal(v, v0) and torch.equal(i, i0) and p.tolist() == p0.tolist()
+    ms2 = [marks[j].elapsed_time(marks[j + 1]) for j in range(4)]
+    assert all(t >= 0 for t in ms + ms2) and ms[2] > 0 and ms2[2] > 0
+    oracle.check_exact(q, x, k, v0.cpu().numpy(), i0.cpu().numpy().astype(np.int64))
+
+
 @pytest.mark.parametrize("b,k", [(1, 10), (1, 200), (64, 10), (256, 100), (16, 256)])
 def test_compaction_under_ascending_scores(eng, b, k):
     """Rows ordered so that every tile beats all previous ones: without a
