@@ -153,7 +153,7 @@ struct Plan {
   int64_t gemv_grid = 0, rows_per_wave = 0;
   // sampling pre-pass
   bool prepass = false;
-  int64_t nsample = 0, units = 0;
+  int64_t nsample = 0, spt = 1, units = 0;
   // workspace
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
 };
@@ -182,12 +182,13 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     P.nlists = waves;
     P.cap = std::max<int64_t>(128, pow2_at_least(k + 8));
     const int64_t nblocks = ceil_div(n, 64);
-    const int64_t s = std::min<int64_t>(1024, std::max<int64_t>(nblocks / 16, ceil_div(2 * k, 64)));
+    // sampled 64-row blocks, 8 units (row classes mod 8) each
+    const int64_t s = std::min<int64_t>(512, std::max<int64_t>(nblocks / 16, ceil_div(2 * k, 8)));
     P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
                 (((flags & CVS_FLAG_FORCE_PREPASS) && s <= nblocks) || (s >= 4 && s <= nblocks / 8));
     if (P.prepass) {
       P.nsample = s;
-      P.units = s * 64;
+      P.units = s * 8;
     }
   } else {
     if (!forced_bq) {
@@ -224,13 +225,21 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
     P.nlists = c * rs;
     P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
+    // Sampling pre-pass: about 1/16 of the tiles, and at least 8k/upt of them
+    // but at most a quarter (its threshold is the k-th best of ~upt*s unit
+    // maxima, so the expected number of candidates that pass it is about
+    // k * ntiles / s), run by at most one workgroup per CU, each on spt
+    // consecutive tiles.
     const int64_t upt = P.cfg.units_per_tile();  // sampling units per tile
-    const int64_t s = std::min<int64_t>(256, std::max<int64_t>(P.ntiles / 16, ceil_div(2 * k, upt)));
+    int64_t s = std::min<int64_t>(1024, std::max<int64_t>(P.ntiles / 16, ceil_div(8 * k, upt)));
+    s = std::min<int64_t>(s, (flags & CVS_FLAG_FORCE_PREPASS) ? P.ntiles : P.ntiles / 4);
     P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
-                (((flags & CVS_FLAG_FORCE_PREPASS) && s <= P.ntiles) || (s >= 4 && s <= P.ntiles / 8));
+                (((flags & CVS_FLAG_FORCE_PREPASS) && s >= 1) || (s >= 4 && s * upt >= 2 * k));
     if (P.prepass) {
-      P.nsample = s;
-      P.units = s * upt;
+      const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(s, cus / P.groups));
+      P.spt = std::max<int64_t>(1, s / wgs);
+      P.nsample = wgs;
+      P.units = wgs * P.spt * upt;
     }
   }
   if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
@@ -388,6 +397,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       ScanArgs pa = a;
       pa.umax = umax;
       pa.nsample = (int)P.nsample;
+      pa.spt = (int)P.spt;
       pa.units = (int)P.units;
       e = launch_scan(P.cfg, kMax, pa, (int)(P.groups * P.nsample), s);
       if (e != hipSuccess) return hip_fail(e, "sample pass launch");

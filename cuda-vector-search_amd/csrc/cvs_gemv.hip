@@ -39,13 +39,11 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
   const int np = d >> 6;
   const int64_t n = a.n;
 
+  // Unconditional loads (a piece past d re-reads the last one and is never
+  // used): a per-load branch would put each behind a wait for the previous one.
   half8 qv[PMAX];
 #pragma unroll
-  for (int p = 0; p < PMAX; ++p) {
-    half8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (p < np) v = *(const half8*)(a.q + p * 64 + sub * 8);
-    qv[p] = v;
-  }
+  for (int p = 0; p < PMAX; ++p) qv[p] = *(const half8*)(a.q + min(p, np - 1) * 64 + sub * 8);
 
   int64_t r_begin, r_end;
   if (MODE == kMax) {
@@ -60,6 +58,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
   }
 
   float thr = (MODE == kAppend && a.tau) ? a.tau[0] : -__builtin_inff();
+  float umax = -__builtin_inff();  // kMax: best score of this lane group's rows
   int count = 0;
   float* lv = nullptr;
   int* li = nullptr;
@@ -91,7 +90,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       const int64_t row = r0 + u * 8 + rg;
       const bool valid = row < r_end;
       if (MODE == kMax) {
-        if (sub == 0) a.umax[(int64_t)gw * 64 + (row - r_begin)] = valid ? acc : -__builtin_inff();
+        if (valid) umax = fmaxf(umax, acc);
       } else {
         bool pass = valid && sub == 0 && acc >= thr;
         uint64_t mask = __ballot(pass);
@@ -114,11 +113,9 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       }
     }
   }
-  if (MODE == kMax) {
-    // rows past the end of a partial sampled block
-    for (int64_t row = r_end + lane; row < r_begin + 64; row += kWave)
-      a.umax[(int64_t)gw * 64 + (row - r_begin)] = -__builtin_inff();
-  }
+  // kMax: sampling unit (block, rg) = the block's rows congruent to rg mod 8;
+  // its maximum is the score of one actual row (or -inf past the corpus end).
+  if (MODE == kMax && sub == 0) a.umax[(int64_t)gw * 8 + rg] = umax;
   if (MODE == kAppend && lane == 0) a.lcount[gw] = count;
 }
 

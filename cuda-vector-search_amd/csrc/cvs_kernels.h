@@ -39,8 +39,9 @@ struct ScanArgs {
   int k;
   // kMax
   float* umax;        // [nq, units]
-  int nsample;        // sampled tiles (one per workgroup)
-  int units;          // units per query = nsample * RS * 4
+  int nsample;        // sampling workgroups per query group
+  int spt;            // consecutive tiles sampled by each of them
+  int units;          // units per query = nsample * spt * units_per_tile
   // kStore*
   void* out;          // [nq, n]
 };
@@ -59,7 +60,7 @@ struct GemvArgs {
   int nlists;         // total waves
   int cap;
   int k;
-  float* umax;        // kMax: [units], one unit per sampled row
+  float* umax;        // kMax: [units], 8 per sampled 64-row block (rows mod 8)
   int nsample;        // kMax: sampled 64-row blocks (one per wave)
   int units;
   int mode;           // kAppend or kMax

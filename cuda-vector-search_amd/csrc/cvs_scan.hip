@@ -67,7 +67,10 @@ struct Mfma<32> {
   __device__ static constexpr int row(int e) { return 8 * (e >> 2) + (e & 3); }
 };
 
-template <int MS, int QS, int QB, int RB, int KSMAX, int MODE>
+// FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
+// compile-time constant (per-stage guards on a runtime count split the
+// unrolled stage loop into separate blocks and cost ~15% of the scan).
+template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
 __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   typedef Mfma<MS> M;
   typedef typename M::acc_t acc_t;
@@ -88,15 +91,19 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
   constexpr bool APP = (MODE == kAppend);
-  constexpr int STCAP = 64;          // staged lane-rows per wave
+  constexpr int STCAP = 64;          // staged entries per wave
+  // A staged entry is one lane's NE scores of one (query block, row block): a
+  // row of EST floats (NE plus padding to an odd number of 16-byte units, so
+  // that ds_write/read_b128 of 16 consecutive entries hit distinct banks).
+  constexpr int EST = ((M::NE / 4) | 1) * 4;
   // Pin the query fragments to AGPRs when they dominate the register budget.
   constexpr bool PIN_Q = QB * KSMAX * 4 >= 128;
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NBUF * STAGE];
   __shared__ int lcnt[RS][BQ];                        // entries in each owned list
   __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
-  __shared__ float st_val[APP ? 4 : 1][APP ? NV : 1][STCAP];  // staged lane-rows, value-major
-  __shared__ int st_meta[APP ? 4 : 1][APP ? 2 * STCAP : 1];       // (query, first row)
+  __shared__ __attribute__((aligned(16))) float st_val[APP ? 4 : 1][APP ? STCAP * EST : 1];  // staged entries
+  __shared__ int st_meta[APP ? 4 : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
   __shared__ uint64_t sortbuf[APP ? 4 * kMaxCap : 1];  // compaction scratch
 
   const int tid = threadIdx.x;
@@ -123,16 +130,19 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     }
   }
   int64_t t_begin, t_end;
-  if (MODE == kMax) {
-    t_begin = ((2 * (int64_t)chunk + 1) * a.ntiles) / (2 * (int64_t)a.nsample);
-    t_end = t_begin + 1;
+  if (MODE == kMax) {  // spt consecutive tiles centred on an evenly spread position
+    const int64_t centre = ((2 * (int64_t)chunk + 1) * a.ntiles) / (2 * (int64_t)a.nsample);
+    t_begin = centre - a.spt / 2;
+    if (t_begin > a.ntiles - a.spt) t_begin = a.ntiles - a.spt;
+    if (t_begin < 0) t_begin = 0;
+    t_end = t_begin + a.spt;
   } else {
     t_begin = (int64_t)chunk * a.tpc;
     t_end = t_begin + a.tpc < a.ntiles ? t_begin + a.tpc : a.ntiles;
   }
 
   const int d = a.d;
-  const int nc = d >> 6;
+  const int nc = FULLW ? NCMAX : (d >> 6);
   const int64_t n = a.n;
   const int qwave0 = grp * BQ + qs * QW;
 
@@ -177,17 +187,26 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i) issue_next();
 
-  // Query fragments (B operand), resident for the whole launch.
+  // Query fragments (B operand), resident for the whole launch.  The loads are
+  // unconditional so that they issue back to back (a per-load lane mask puts
+  // each behind a wait for the previous one): a column past nq loads query
+  // nq-1 (its scores are never reported: its threshold is +inf and kMax skips
+  // it), a k-step past d loads the last one (the stage loop never uses it).
   half8 qf[QB][KSMAX];
+  {
+    half8 ld[QB][KSMAX];
+    const int ksl = d / M::KSZ - 1;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qi = qwave0 + qb * MS + col;
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qi = min(qwave0 + qb * MS + col, a.nq - 1);
 #pragma unroll
-    for (int ks = 0; ks < KSMAX; ++ks) {
-      half8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (qi < a.nq && ks * M::KSZ < d) v = *(const half8*)(a.q + (int64_t)qi * d + ks * M::KSZ + kg * 8);
-      qf[qb][ks] = PIN_Q ? pin_agpr(v) : v;
+      for (int ks = 0; ks < KSMAX; ++ks)
+        ld[qb][ks] = *(const half8*)(a.q + (int64_t)qi * d + min(ks, ksl) * M::KSZ + kg * 8);
     }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < KSMAX; ++ks) qf[qb][ks] = PIN_Q ? pin_agpr(ld[qb][ks]) : ld[qb][ks];
   }
 
   float thr[QB];
@@ -205,7 +224,7 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   }
   int st_n = 0;  // wave-uniform count of staged lane-rows
 
-  // Appends the passing scores of this wave's staged lane-rows to its global
+  // Appends the passing scores of this wave's staged entries to its global
   // candidate lists.  A list that fills up is compacted to its k best entries
   // (raising that query's threshold) and the remaining scores are retried.
   auto flush = [&]() {
@@ -214,33 +233,41 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     for (int base = 0; base < st_n; base += kWave) {
       const int er = base + lane;
       const bool have = er < st_n;
+      const int ers = have ? er : 0;
       const int ql = have ? st_meta[w][2 * er] : 0;
       const int rbase = have ? st_meta[w][2 * er + 1] : 0;
-      const int ers = have ? er : 0;
+      float ev[M::NE];
+#pragma unroll
+      for (int c = 0; c < M::NE / 4; ++c) {
+        const f32x4 t = *(const f32x4*)(&st_val[w][ers * EST + 4 * c]);
+        ev[4 * c] = t[0];
+        ev[4 * c + 1] = t[1];
+        ev[4 * c + 2] = t[2];
+        ev[4 * c + 3] = t[3];
+      }
       const int64_t lbase = ((int64_t)(grp * BQ + ql) * a.nlists + list) * a.cap;
-      int next = have ? 0 : NV;  // first score of this lane-row not yet handled
+      unsigned todo = 0;  // scores of this entry not yet appended
+      if (have) {
+        const float tq = thr_s[rs][ql];
+#pragma unroll
+        for (int e = 0; e < M::NE; ++e) todo |= (ev[e] >= tq ? 1u : 0u) << e;
+      }
 #pragma unroll 1
       while (true) {
-        const float tq = thr_s[rs][ql];
-        int cnt = 0;
-#pragma unroll 1
-        for (int e = next; e < NV; ++e) cnt += (st_val[w][e][ers] >= tq) ? 1 : 0;
+        const int cnt = __popc(todo);
         const int pos = cnt ? atomicAdd(&lcnt[rs][ql], cnt) : 0;
         const int room = a.cap - pos;
         int put = 0;
-        int e = next;
-#pragma unroll 1
-        for (; e < NV && put < room; ++e) {
-          const float v = st_val[w][e][ers];
-          if (v >= tq) {
-            a.lv[lbase + pos + put] = v;
-            a.li[lbase + pos + put] = rbase + (e / M::NE) * MS + M::row(e % M::NE);
+#pragma unroll
+        for (int e = 0; e < M::NE; ++e) {
+          if (((todo >> e) & 1u) && put < room) {
+            a.lv[lbase + pos + put] = ev[e];
+            a.li[lbase + pos + put] = rbase + M::row(e);
+            todo &= ~(1u << e);
             ++put;
           }
         }
-        const bool over = put < cnt;
-        next = over ? e : NV;
-        uint64_t om = __ballot(over);
+        uint64_t om = __ballot(todo != 0);
         if (!om) break;
 #pragma unroll 1
         while (om) {
@@ -255,6 +282,13 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
             thr_s[rs][ql0] = nt;
           }
           om &= ~__ballot(ql == ql0);
+        }
+        // drop the scores that no longer pass the raised threshold
+        if (todo) {
+          const float tq = thr_s[rs][ql];
+#pragma unroll
+          for (int e = 0; e < M::NE; ++e)
+            if (ev[e] < tq) todo &= ~(1u << e);
         }
       }
     }
@@ -356,26 +390,36 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
           }
         }
       } else {
-        float m = v[0];
-#pragma unroll
-        for (int j = 1; j < NV; ++j) m = fmaxf(m, v[j]);
         if (MODE == kMax) {
-          if (qi < a.nq) a.umax[(int64_t)qi * a.units + chunk * (RS * G) + rs * G + kg] = m;
-        } else {  // kAppend
-          uint64_t mk = __ballot(m >= thr[qb]);
-          if (mk) {
-            if (st_n + __popcll(mk) > STCAP) {
-              flush();
-              mk = __ballot(m >= thr[qb]);
-            }
-            if (m >= thr[qb]) {
-              const int p = st_n + lanes_below(mk);
+          float m = v[0];
 #pragma unroll
-              for (int j = 0; j < NV; ++j) st_val[w][j][p] = v[j];
-              st_meta[w][2 * p] = qs * QW + qb * MS + col;
-              st_meta[w][2 * p + 1] = (int)rowb;
+          for (int j = 1; j < NV; ++j) m = fmaxf(m, v[j]);
+          if (qi < a.nq)
+            a.umax[(int64_t)qi * a.units + ((chunk * a.spt + (t - t_begin)) * RS + rs) * G + kg] = m;
+        } else {  // kAppend: stage each row block whose maximum passes
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {
+            float m = v[rb * M::NE];
+#pragma unroll
+            for (int e = 1; e < M::NE; ++e) m = fmaxf(m, v[rb * M::NE + e]);
+            uint64_t mk = __ballot(m >= thr[qb]);
+            if (mk) {
+              if (st_n + __popcll(mk) > STCAP) {
+                flush();
+                mk = __ballot(m >= thr[qb]);
+              }
+              if (m >= thr[qb]) {
+                const int p = st_n + lanes_below(mk);
+#pragma unroll
+                for (int c = 0; c < M::NE / 4; ++c)
+                  *(f32x4*)(&st_val[w][p * EST + 4 * c]) =
+                      f32x4{v[rb * M::NE + 4 * c], v[rb * M::NE + 4 * c + 1], v[rb * M::NE + 4 * c + 2],
+                            v[rb * M::NE + 4 * c + 3]};
+                st_meta[w][2 * p] = qs * QW + qb * MS + col;
+                st_meta[w][2 * p + 1] = (int)rowb + rb * MS;
+              }
+              st_n += __popcll(mk);
             }
-            st_n += __popcll(mk);
           }
         }
       }
@@ -399,18 +443,25 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
 
 template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
+  const bool full = (a.d == KS * Mfma<MS>::KSZ);
   switch (mode) {
     case kAppend:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend>), dim3(grid), dim3(kBlock), 0, s, a);
+      if (full)
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(kBlock), 0, s, a);
+      else
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kMax:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax>), dim3(grid), dim3(kBlock), 0, s, a);
+      if (full)
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(kBlock), 0, s, a);
+      else
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kStoreF32:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     case kStoreF16:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(kBlock), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;
