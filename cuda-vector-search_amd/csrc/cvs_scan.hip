@@ -88,6 +88,8 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   constexpr int NBUF = ((QS == 4 ? 56 : 40) * 1024) / STAGE + 2;
   static_assert((NBUF - 2) * LPW < 64 && NBUF >= 3, "vmcnt budget / pipeline depth");
   constexpr int NCMAX = KSMAX / KPS; // 64-column stages per tile (max)
+  // One barrier per two stages when every tile has the same, even stage count.
+  constexpr bool PAIR = FULLW && (NCMAX % 2 == 0) && NBUF >= 5;
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
   constexpr bool APP = (MODE == kAppend);
@@ -330,12 +332,21 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
 #pragma unroll
     for (int c = 0; c < NCMAX; ++c) {
       if (c < nc) {
-        // Stage s is in ab[c & 1].  Wait until stage s+1 has landed for every
-        // wave; the barrier also retires all reads of stage s-1's buffer, which
-        // issue_next() refills with stage s+NBUF-1.
-        wait_vmcnt_lgkm0<(NBUF - 3) * LPW>();
-        __builtin_amdgcn_s_barrier();
-        issue_next();
+        // Stage s is in ab[c & 1].  Per-stage sync: wait until stage s+1 has
+        // landed for every wave; the barrier also retires all reads of stage
+        // s-1's buffer, which issue_next() refills with stage s+NBUF-1.  Paired
+        // sync (even s only): wait for stages s+1 and s+2, then refill the
+        // buffers of stages s-1 and s with stages s+NBUF-1 and s+NBUF.
+        if (!PAIR) {
+          wait_vmcnt_lgkm0<(NBUF - 3) * LPW>();
+          __builtin_amdgcn_s_barrier();
+          issue_next();
+        } else if ((c & 1) == 0) {
+          wait_vmcnt_lgkm0<(NBUF - 4) * LPW>();
+          __builtin_amdgcn_s_barrier();
+          issue_next();
+          issue_next();
+        }
         const int nxt = (cur_buf + 1 == NBUF) ? 0 : cur_buf + 1;
         read_stage(nxt, ab[(c + 1) & 1]);
 #pragma unroll
