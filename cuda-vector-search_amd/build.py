@@ -37,6 +37,11 @@ FLAGS = [
 
 SOURCES = ["cvs_scan.hip", "cvs_select.hip", "cvs_gemv.hip", "cvs_capi.hip"]
 
+# Per-source extra flags.  The scan keeps its MFMA accumulators in VGPRs (the
+# query fragments are pinned in AGPRs explicitly): the epilogue then reads the
+# scores without 64 v_accvgpr_read per tile (measured 3-6% faster scan).
+EXTRA = {"cvs_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def _run(cmd, verbose):
     if verbose:
@@ -55,7 +60,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     for src in SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([HIPCC, *FLAGS, "-c", CSRC / src, "-o", obj])
+        cmds.append([HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", CSRC / src, "-o", obj])
     with ThreadPoolExecutor(max_workers=jobs or min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB.with_suffix(".so.tmp")
