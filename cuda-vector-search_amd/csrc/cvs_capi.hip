@@ -154,6 +154,7 @@ struct Plan {
   // sampling pre-pass
   bool prepass = false;
   int64_t nsample = 0, spt = 1, units = 0;
+  int agg = 0;
   // workspace
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
 };
@@ -239,7 +240,11 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
       const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(s, cus / P.groups));
       P.spt = std::max<int64_t>(1, s / wgs);
       P.nsample = wgs;
-      P.units = wgs * P.spt * upt;
+      // One unit per (workgroup, row split, lane group) when that still leaves
+      // >= 32k units (the top k scores then almost never share a unit, so the
+      // threshold is as tight as per-tile units give, from fewer values).
+      P.agg = (P.spt > 1 && wgs * upt >= 32 * k) ? 1 : 0;
+      P.units = wgs * (P.agg ? 1 : P.spt) * upt;
     }
   }
   if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
@@ -398,6 +403,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       pa.umax = umax;
       pa.nsample = (int)P.nsample;
       pa.spt = (int)P.spt;
+      pa.agg = P.agg;
       pa.units = (int)P.units;
       e = launch_scan(P.cfg, kMax, pa, (int)(P.groups * P.nsample), s);
       if (e != hipSuccess) return hip_fail(e, "sample pass launch");

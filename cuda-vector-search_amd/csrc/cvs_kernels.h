@@ -41,7 +41,8 @@ struct ScanArgs {
   float* umax;        // [nq, units]
   int nsample;        // sampling workgroups per query group
   int spt;            // consecutive tiles sampled by each of them
-  int units;          // units per query = nsample * spt * units_per_tile
+  int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles
+  int units;          // units per query = nsample * (agg ? 1 : spt) * units_per_tile
   // kStore*
   void* out;          // [nq, n]
 };

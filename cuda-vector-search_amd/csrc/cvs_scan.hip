@@ -225,6 +225,9 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     }
   }
   int st_n = 0;  // wave-uniform count of staged lane-rows
+  float umx[QB];  // kMax with agg: this lane's unit maxima over all sampled tiles
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) umx[qb] = -__builtin_inff();
 
   // Appends the passing scores of this wave's staged entries to its global
   // candidate lists.  A list that fills up is compacted to its k best entries
@@ -405,7 +408,9 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
           float m = v[0];
 #pragma unroll
           for (int j = 1; j < NV; ++j) m = fmaxf(m, v[j]);
-          if (qi < a.nq)
+          if (a.agg)
+            umx[qb] = fmaxf(umx[qb], m);
+          else if (qi < a.nq)
             a.umax[(int64_t)qi * a.units + ((chunk * a.spt + (t - t_begin)) * RS + rs) * G + kg] = m;
         } else {  // kAppend: stage each row block whose maximum passes
 #pragma unroll
@@ -437,6 +442,13 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     }
   }
   if (APP && st_n > 0) flush();
+  if (MODE == kMax && a.agg) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qi = qwave0 + qb * MS + col;
+      if (qi < a.nq) a.umax[(int64_t)qi * a.units + (chunk * RS + rs) * G + kg] = umx[qb];
+    }
+  }
 
   // Drain the trailing (dummy) stage loads before this workgroup's LDS can be
   // handed to another one, and make all list counts final.
