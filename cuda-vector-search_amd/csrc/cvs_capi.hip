@@ -155,6 +155,7 @@ struct Plan {
   bool prepass = false;
   int64_t nsample = 0, spt = 1, units = 0;
   int agg = 0;
+  int upb = 8;  // gemv sampling units per block
   // workspace
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
 };
@@ -189,7 +190,8 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
                 (((flags & CVS_FLAG_FORCE_PREPASS) && s <= nblocks) || (s >= 4 && s <= nblocks / 8));
     if (P.prepass) {
       P.nsample = s;
-      P.units = s * 8;
+      P.upb = (s >= 32 * k) ? 1 : 8;  // whole-block units when they are plentiful
+      P.units = s * P.upb;
     }
   } else {
     if (!forced_bq) {
@@ -358,6 +360,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       pg.mode = kMax;
       pg.umax = umax;
       pg.nsample = (int)P.nsample;
+      pg.upb = P.upb;
       pg.units = (int)P.units;
       e = launch_gemv(ks_bucket(d) * 32, pg, (int)ceil_div(P.nsample, 4), s);
       if (e != hipSuccess) return hip_fail(e, "gemv sample pass launch");

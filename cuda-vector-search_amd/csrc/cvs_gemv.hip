@@ -113,9 +113,19 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       }
     }
   }
-  // kMax: sampling unit (block, rg) = the block's rows congruent to rg mod 8;
-  // its maximum is the score of one actual row (or -inf past the corpus end).
-  if (MODE == kMax && sub == 0) a.umax[(int64_t)gw * 8 + rg] = umax;
+  // kMax: sampling unit (block, rg) = the block's rows congruent to rg mod 8, or
+  // the whole block when upb == 1; its maximum is the score of one actual row
+  // (or -inf past the corpus end).
+  if (MODE == kMax) {
+    if (a.upb == 1) {  // one unit per block: the maximum over its 8 row classes
+      umax = fmaxf(umax, __shfl_xor(umax, 8));
+      umax = fmaxf(umax, __shfl_xor(umax, 16));
+      umax = fmaxf(umax, __shfl_xor(umax, 32));
+      if (lane == 0) a.umax[gw] = umax;
+    } else if (sub == 0) {
+      a.umax[(int64_t)gw * 8 + rg] = umax;
+    }
+  }
   if (MODE == kAppend && lane == 0) a.lcount[gw] = count;
 }
 

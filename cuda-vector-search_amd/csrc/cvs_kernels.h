@@ -61,8 +61,9 @@ struct GemvArgs {
   int nlists;         // total waves
   int cap;
   int k;
-  float* umax;        // kMax: [units], 8 per sampled 64-row block (rows mod 8)
+  float* umax;        // kMax: [units], upb per sampled 64-row block
   int nsample;        // kMax: sampled 64-row blocks (one per wave)
+  int upb;            // kMax: units per block, 8 (rows mod 8) or 1 (the block)
   int units;
   int mode;           // kAppend or kMax
 };
