@@ -308,7 +308,7 @@ namespace {
 // or GEMV, 3 final select; skipped stages get back-to-back marks.
 int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq,
               int64_t chunks, int flags, void* workspace, int64_t workspace_bytes, float* out_v,
-              int32_t* out_i, int64_t* plan_out, int device, void* stream, hipEvent_t* marks) {
+              void* out_i, int64_t* plan_out, int device, void* stream, hipEvent_t* marks) {
   DevInfo di;
   int rc = dev_info(device, &di);
   if (rc != CVS_OK) return rc;
@@ -442,6 +442,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
   fa.k = (int)k;
   fa.out_v = out_v;
   fa.out_i = out_i;
+  fa.ids64 = (flags & CVS_FLAG_IDS_INT64) ? 1 : 0;
   e = launch_select(0, fa, (int)nq, s);
   if (e != hipSuccess) return hip_fail(e, "select launch");
   mark(4);
@@ -454,14 +455,14 @@ extern "C" {
 
 int cvs_fused_topk(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                    int64_t bq, int64_t chunks, int flags, void* workspace, int64_t workspace_bytes,
-                   float* out_v, int32_t* out_i, int64_t* plan_out, int device, void* stream) {
+                   float* out_v, void* out_i, int64_t* plan_out, int device, void* stream) {
   return run_fused(q, x, nq, n, d, k, bq, chunks, flags, workspace, workspace_bytes, out_v, out_i,
                    plan_out, device, stream, nullptr);
 }
 
 int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                          int64_t bq, int64_t chunks, int flags, void* workspace,
-                         int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                         int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,
                          int device, void* stream, float* stage_ms) {
   if (stage_ms == nullptr) return fail(CVS_ERR_INVALID, "stage_ms must not be null");
   for (int i = 0; i < 4; ++i) stage_ms[i] = 0.f;
@@ -491,7 +492,7 @@ int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, in
 
 int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                           int64_t bq, int64_t chunks, int flags, void* workspace,
-                          int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                          int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,
                           int device, void* stream, void* const* marks) {
   if (marks == nullptr) return fail(CVS_ERR_INVALID, "marks must not be null");
   hipEvent_t ev[5];

@@ -77,7 +77,8 @@ struct SelectArgs {
   int cap;
   int k;
   float* out_v;        // [nq, k] (final mode)
-  int* out_i;          // [nq, k] (final mode)
+  void* out_i;         // [nq, k] int32, or int64 when ids64 (final mode)
+  int ids64;
   float* tau;          // [nq]    (threshold mode: score of the k-th best)
 };
 

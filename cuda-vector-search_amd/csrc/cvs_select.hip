@@ -226,7 +226,11 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
     for (int r = tid; r < k; r += kBlock) {
       const bool ok = r < nb;
       a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
-      a.out_i[(int64_t)q * k + r] = ok ? key_id(S.keys[r]) : -1;
+      const int id = ok ? key_id(S.keys[r]) : -1;
+      if (a.ids64)
+        ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
+      else
+        ((int*)a.out_i)[(int64_t)q * k + r] = id;
     }
   }
 }

@@ -30,6 +30,7 @@ ARCH = "gfx950"
 FLAG_NO_PREPASS = 1
 FLAG_FORCE_PREPASS = 2
 FLAG_NO_GEMV = 4
+FLAG_IDS_INT64 = 8  # ids as int64 (Index.search's dtype) instead of the reference's int32
 
 
 def available() -> bool:
@@ -187,7 +188,7 @@ class Engine:
         if rc != 0:
             raise self._error(rc)
         out_v = torch.empty((nq, k), dtype=torch.float32, device=dev)
-        out_i = torch.empty((nq, k), dtype=torch.int32, device=dev)
+        out_i = torch.empty((nq, k), dtype=torch.int64 if flags & FLAG_IDS_INT64 else torch.int32, device=dev)
         plan = torch.tensor([int(plan_c[0]), int(plan_c[1])], dtype=torch.int64)
         if nq == 0:
             return [out_v, out_i, plan]

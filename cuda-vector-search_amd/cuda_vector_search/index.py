@@ -127,8 +127,9 @@ class Index:
         if method == "fused":
             if k > MAX_FUSED_K:
                 raise ValueError(f"fused search supports k <= {MAX_FUSED_K}")
-            v, i, _ = _ext.load().fused_topk(q, self._x, k)
-            return v, i.long()
+            # ids come out as int64 directly (index.py:126 widens int32 with .long())
+            v, i, _ = _ext.load().fused_topk(q, self._x, k, flags=_ext.FLAG_IDS_INT64)
+            return v, i
         if method == "twopass":
             s = _ext.load().scores(q, self._x, False)
             v, i = torch.topk(s, k, dim=1)

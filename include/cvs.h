@@ -45,6 +45,7 @@ extern "C" {
 #define CVS_FLAG_NO_PREPASS 1    /* skip the sampling pre-pass (threshold starts at -inf) */
 #define CVS_FLAG_FORCE_PREPASS 2 /* run the pre-pass whenever it is well defined */
 #define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
+#define CVS_FLAG_IDS_INT64 8     /* out_i is int64 (the dtype Index.search returns, index.py:126) */
 
 /* Library version (CVS_VERSION). */
 int cvs_version(void);
@@ -81,8 +82,9 @@ int cvs_fused_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int6
 /*
  * Exact top-k by inner product: for each query, the k rows with the largest
  * fp32-accumulated score, sorted by score descending and then row id
- * ascending.  out_v is [nq, k] fp32, out_i is [nq, k] int32.  Requires
- * 1 <= k <= 256 and k <= n.  `workspace` (256-byte aligned) must hold at least
+ * ascending.  out_v is [nq, k] fp32, out_i is [nq, k] int32 (int64 with
+ * CVS_FLAG_IDS_INT64).  Requires 1 <= k <= 256 and k <= n.  `workspace`
+ * (256-byte aligned) must hold at least
  * the bytes cvs_fused_plan reports for the same arguments; its contents need
  * no initialisation.  plan_out (may be NULL) receives the plan as in
  * cvs_fused_plan.  Replaces fused_topk() of kernels.cu:501-582 (Index.search
@@ -90,7 +92,7 @@ int cvs_fused_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int6
  */
 int cvs_fused_topk(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                    int64_t bq, int64_t chunks, int flags, void* workspace, int64_t workspace_bytes,
-                   float* out_v, int32_t* out_i, int64_t* plan_out, int device, void* stream);
+                   float* out_v, void* out_i, int64_t* plan_out, int device, void* stream);
 
 /*
  * Diagnostic twin of cvs_fused_topk (no counterpart in the reference): runs
@@ -103,7 +105,7 @@ int cvs_fused_topk(const void* q, const void* x, int64_t nq, int64_t n, int64_t 
  */
 int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                          int64_t bq, int64_t chunks, int flags, void* workspace,
-                         int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                         int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,
                          int device, void* stream, float* stage_ms);
 
 /*
@@ -116,7 +118,7 @@ int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, in
  */
 int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                           int64_t bq, int64_t chunks, int flags, void* workspace,
-                          int64_t workspace_bytes, float* out_v, int32_t* out_i, int64_t* plan_out,
+                          int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,
                           int device, void* stream, void* const* marks);
 
 #ifdef __cplusplus

@@ -71,6 +71,7 @@ def test_python_flags_match_header():
     assert _ext.FLAG_NO_PREPASS == int(d["CVS_FLAG_NO_PREPASS"])
     assert _ext.FLAG_FORCE_PREPASS == int(d["CVS_FLAG_FORCE_PREPASS"])
     assert _ext.FLAG_NO_GEMV == int(d["CVS_FLAG_NO_GEMV"])
+    assert _ext.FLAG_IDS_INT64 == int(d["CVS_FLAG_IDS_INT64"])
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU behaviour")

@@ -268,6 +268,22 @@ def test_timed_and_marked_twins_match(eng, n, d, b, k):
     oracle.check_exact(q, x, k, v0.cpu().numpy(), i0.cpu().numpy().astype(np.int64))
 
 
+@pytest.mark.parametrize("n,d,b,k", [(30000, 384, 64, 10), (50000, 768, 1, 25)])
+def test_int64_ids_flag(eng, n, d, b, k):
+    """CVS_FLAG_IDS_INT64 (what Index.search uses) writes the same ids as int64."""
+    say(f"int64 ids n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=9)
+    qd, xd = q.cuda(), x.cuda()
+    v32, i32, _ = eng.fused_topk(qd, xd, k)
+    v64, i64, _ = eng.fused_topk(qd, xd, k, flags=_ext.FLAG_IDS_INT64)
+    torch.cuda.synchronize()
+    assert i32.dtype == torch.int32 and i64.dtype == torch.int64
+    assert torch.equal(v32, v64) and torch.equal(i32.long(), i64)
+    index = Index(xd, metric="ip", copy=False)
+    vi, ii = index.search(qd, k)
+    assert ii.dtype == torch.int64 and torch.equal(ii, i64) and torch.equal(vi, v64)
+
+
 @pytest.mark.parametrize("b,k", [(1, 10), (1, 200), (64, 10), (256, 100), (16, 256)])
 def test_compaction_under_ascending_scores(eng, b, k):
     """Rows ordered so that every tile beats all previous ones: without a
