@@ -101,7 +101,10 @@ int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
 
 // Scan configuration for a query block of `bq` queries at width d (false if
 // none).  32x32x16 MFMA (full-rate on gfx950) whenever the queries of a wave
-// fit in VGPRs with it; 16x16x32 for bq = 16 and for rows wider than 768.
+// fit in registers with it; 16x16x32 for bq = 16 and for rows wider than 768.
+// bq = 256 at d <= 384 runs 8 waves (32 queries each, two per SIMD), so that
+// one wave's candidate epilogue and barrier waits overlap the other's MFMAs
+// (measured 7% faster than 4 waves of 64 queries).
 bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
   switch (bq) {
     case 16:
@@ -122,7 +125,7 @@ bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
       if (d <= 768) { *c = {32, 4, 1, 2, 48}; return true; }
       return false;
     case 256:
-      if (d <= 384) { *c = {32, 4, 2, 2, 24}; return true; }
+      if (d <= 384) { *c = {32, 8, 1, 2, 24}; return true; }  // 8 waves, 2 per SIMD
       return false;
     default:
       return false;

@@ -87,7 +87,7 @@ struct SelectArgs {
 struct ScanCfg {
   int ms, qs, qb, rb, ksmax;
   int bq() const { return qs * ms * qb; }
-  int rs() const { return 4 / qs; }
+  int rs() const { return qs >= 4 ? 1 : 4 / qs; }  // row splits (waves = qs * rs)
   int tile_rows() const { return rs() * rb * ms; }
   int wave_rows() const { return rb * ms; }
   int dmax() const { return ksmax * (ms == 16 ? 32 : 16); }

@@ -4,10 +4,11 @@
 // kernels.cu:313-371 (and the score kernel, kernels.cu:285-311), re-designed
 // for gfx950:
 //
-//  * 256 threads = 4 wave64s, one per SIMD.  Queries are split QS ways across
-//    the waves and tile rows RS = 4/QS ways.  Each wave keeps its QW = MS*QB
-//    queries as MFMA B fragments in VGPRs for the whole launch (loaded once), so
-//    the corpus is the only operand that streams.
+//  * 256 threads = 4 wave64s, one per SIMD (QS <= 4), or 512 threads = 8
+//    wave64s, two per SIMD (QS = 8).  Queries are split QS ways across the
+//    waves and tile rows RS = 4/QS ways.  Each wave keeps its QW = MS*QB
+//    queries as MFMA B fragments in registers (AGPRs) for the whole launch
+//    (loaded once), so the corpus is the only operand that streams.
 //  * MFMA shape MS = 32 (v_mfma_f32_32x32x16_f16) wherever the query block
 //    allows it: on gfx950 it runs at the full dense fp16 rate, twice the
 //    throughput of v_mfma_f32_16x16x32_f16, which is kept (MS = 16) for batch
@@ -71,10 +72,12 @@ struct Mfma<32> {
 // compile-time constant (per-stage guards on a runtime count split the
 // unrolled stage loop into separate blocks and cost ~15% of the scan).
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
-__global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
+__global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a) {
   typedef Mfma<MS> M;
   typedef typename M::acc_t acc_t;
-  constexpr int RS = 4 / QS;
+  constexpr int RS = QS >= 4 ? 1 : 4 / QS;  // row splits
+  constexpr int NW = QS * RS;       // waves: 4 (one per SIMD) or 8 (two per SIMD)
+  constexpr int NT = NW * kWave;
   constexpr int QW = MS * QB;        // queries per wave
   constexpr int BQ = QS * QW;        // queries per workgroup
   constexpr int RW = MS * RB;        // rows per wave per tile
@@ -82,10 +85,10 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   constexpr int KPS = 64 / M::KSZ;   // MFMA k-steps per 64-column stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
   constexpr int FPS = TRB * KPS;     // A fragments (1 KB each) per stage
-  static_assert(FPS % 4 == 0, "every wave must issue the same number of stage loads");
-  constexpr int LPW = FPS / 4;       // stage loads per wave
+  static_assert(FPS % NW == 0, "every wave must issue the same number of stage loads");
+  constexpr int LPW = FPS / NW;      // stage loads per wave
   constexpr int STAGE = FPS * 1024;
-  constexpr int NBUF = ((QS == 4 ? 56 : 40) * 1024) / STAGE + 2;
+  constexpr int NBUF = ((QS >= 4 ? 56 : 40) * 1024) / STAGE + 2;
   static_assert((NBUF - 2) * LPW < 64 && NBUF >= 3, "vmcnt budget / pipeline depth");
   constexpr int NCMAX = KSMAX / KPS; // 64-column stages per tile (max)
   // One barrier per two stages when every tile has the same, even stage count.
@@ -99,14 +102,14 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   // that ds_write/read_b128 of 16 consecutive entries hit distinct banks).
   constexpr int EST = ((M::NE / 4) | 1) * 4;
   // Pin the query fragments to AGPRs when they dominate the register budget.
-  constexpr bool PIN_Q = QB * KSMAX * 4 >= 128;
+  constexpr bool PIN_Q = QB * KSMAX * 4 >= 128 || NW == 8;
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NBUF * STAGE];
   __shared__ int lcnt[RS][BQ];                        // entries in each owned list
   __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
-  __shared__ __attribute__((aligned(16))) float st_val[APP ? 4 : 1][APP ? STCAP * EST : 1];  // staged entries
-  __shared__ int st_meta[APP ? 4 : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
-  __shared__ uint64_t sortbuf[APP ? 4 * kMaxCap : 1];  // compaction scratch
+  __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
+  __shared__ int st_meta[APP ? NW : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
+  __shared__ uint64_t sortbuf[APP ? NW * kMaxCap : 1];  // compaction scratch
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   int64_t src_row[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
-    const int f = w + 4 * j;
+    const int f = w + NW * j;
     src_row[j] = t_begin * TR + (f % TRB) * MS + col;
     src[j] = a.x + src_row[j] * d + (f / TRB) * M::KSZ + kg * 8;
   }
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     const bool whole = (it_t + 1) * TR <= n;  // every row of this tile exists
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int f = w + 4 * j;
+      const int f = w + NW * j;
       const _Float16* p = src[j] + it_c * 64;
       if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * 64 + (f / TRB) * M::KSZ + kg * 8;
       dma_to_lds_16(p, buf + f * 1024);
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
     thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
   }
   if (APP) {
-    for (int i = tid; i < RS * BQ; i += kBlock) {
+    for (int i = tid; i < RS * BQ; i += NT) {
       (&lcnt[0][0])[i] = 0;
       const int qi = grp * BQ + i % BQ;
       (&thr_s[0][0])[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
@@ -455,7 +458,7 @@ __global__ __launch_bounds__(kBlock, 1) void scan_kernel(ScanArgs a) {
   wait_vmcnt_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
   if (APP) {
-    for (int i = tid; i < RS * BQ; i += kBlock) {
+    for (int i = tid; i < RS * BQ; i += NT) {
       const int r = i / BQ;
       const int ql = i % BQ;
       const int qi = grp * BQ + ql;
@@ -470,21 +473,21 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   switch (mode) {
     case kAppend:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     case kMax:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     case kStoreF32:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     case kStoreF16:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;
@@ -506,7 +509,7 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   X(32, 2, 1, 1, 48)        \
   X(32, 4, 1, 2, 24)        \
   X(32, 4, 1, 2, 48)        \
-  X(32, 4, 2, 2, 24)
+  X(32, 8, 1, 2, 24)
 
 }  // namespace
 
