@@ -547,4 +547,36 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   return CVS_OK;
 }
 
+int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_stride, int64_t dst_width,
+                  int normalize, int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  if (d < 1 || d > 1536) return fail(CVS_ERR_INVALID, "row width %lld must be in [1, 1536]", (long long)d);
+  if (dst_width < d || dst_width > 1536)
+    return fail(CVS_ERR_INVALID, "destination width %lld must be in [d, 1536]", (long long)dst_width);
+  if (src_stride < d) return fail(CVS_ERR_INVALID, "source row stride must be >= d");
+  if (n < 0) return fail(CVS_ERR_INVALID, "row count must be >= 0");
+  if (n == 0) return CVS_OK;
+  if (src == nullptr || dst == nullptr) return fail(CVS_ERR_INVALID, "row pointers must not be null");
+  if (reinterpret_cast<uintptr_t>(src) % 2 != 0 || reinterpret_cast<uintptr_t>(dst) % 2 != 0)
+    return fail(CVS_ERR_INVALID, "rows must be fp16-aligned");
+  if (src == dst && src_stride != dst_width)
+    return fail(CVS_ERR_INVALID, "in-place preparation needs src_stride == dst_width");
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  PrepArgs a{};
+  a.src = static_cast<const _Float16*>(src);
+  a.dst = static_cast<_Float16*>(dst);
+  a.n = n;
+  a.src_stride = src_stride;
+  a.d = (int)d;
+  a.dst_width = (int)dst_width;
+  a.normalize = normalize ? 1 : 0;
+  hipError_t e = launch_prep(a, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "row preparation launch");
+  return CVS_OK;
+}
+
 }  // extern "C"

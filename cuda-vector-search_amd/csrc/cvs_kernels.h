@@ -68,6 +68,18 @@ struct GemvArgs {
   int mode;           // kAppend or kMax
 };
 
+// Row preparation: dst[r, :d] = src[r, :d] (scaled to unit L2 norm when
+// normalize), dst[r, d:width] = 0.
+struct PrepArgs {
+  const _Float16* src;
+  _Float16* dst;
+  int64_t n;
+  int64_t src_stride;  // elements between source rows (>= d)
+  int d;
+  int dst_width;       // elements per destination row (>= d)
+  int normalize;
+};
+
 // Exact selection over candidate lists: one workgroup per query.
 struct SelectArgs {
   const float* lv;     // [nq, nlists, cap]
@@ -98,6 +110,7 @@ struct ScanCfg {
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
 hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
 hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s);
+hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
 
 bool scan_cfg_available(const ScanCfg& cfg, int mode);
 

@@ -66,6 +66,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.cvs_fused_topk_timed.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                          vp, vp, ctypes.POINTER(i64), i32, vp,
                                          ctypes.POINTER(ctypes.c_float)]
+    lib.cvs_prep_rows.restype = i32
+    lib.cvs_prep_rows.argtypes = [vp, vp, i64, i64, i64, i64, i32, i32, vp]
     lib.cvs_fused_topk_marked.restype = i32
     lib.cvs_fused_topk_marked.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                           vp, vp, ctypes.POINTER(i64), i32, vp,
@@ -124,6 +126,25 @@ class Engine:
         import torch
 
         return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    # -- row preparation (index.py:27-41 on the GPU) ----------------------------
+    def prep_rows(self, src, dst, normalize: bool) -> None:
+        """dst[:, :d] = src (L2-normalised when `normalize`), dst[:, d:] = 0, in one
+        kernel.  src: [n, d] fp16 CUDA rows with unit column stride; dst: [n, w]
+        contiguous fp16, w >= d; dst may be src itself (in place, w == d)."""
+        import torch
+
+        if not (src.is_cuda and dst.is_cuda and src.dtype == torch.float16 and dst.dtype == torch.float16):
+            raise RuntimeError("prep_rows needs fp16 CUDA tensors")
+        if src.dim() != 2 or dst.dim() != 2 or src.shape[0] != dst.shape[0] or src.stride(1) != 1:
+            raise RuntimeError("prep_rows needs [n, d] rows with unit column stride")
+        if not dst.is_contiguous():
+            raise RuntimeError("prep_rows needs a contiguous destination")
+        n, d = src.shape
+        rc = self.lib.cvs_prep_rows(src.data_ptr(), dst.data_ptr(), n, d, src.stride(0), dst.shape[1],
+                                    1 if normalize else 0, src.device.index, self._stream(src.device))
+        if rc != 0:
+            raise self._error(rc)
 
     # -- reference API -------------------------------------------------------
     def scores(self, q, x, out_fp32: bool = True):

@@ -77,10 +77,23 @@ class Index:
         if copy and x.data_ptr() == src.data_ptr():  # .to() returned the caller's storage
             x = x.clone()
         x = x.contiguous()
-        if metric == "cosine":
-            _normalize_(x)
-        self._x = _padded(x) if on_gpu else x
         self._use_kernels = on_gpu and _ext.available()
+        if self._use_kernels and x.shape[1] <= MAX_KERNEL_WIDTH:
+            # one HIP pass each: normalise in place (the caller's tensor too when
+            # copy=False, as in the reference), then zero-pad into a new tensor
+            eng = _ext.load()
+            if metric == "cosine" and x.shape[0] > 0:
+                eng.prep_rows(x, x, True)
+            width = x.shape[1] + (-x.shape[1]) % PAD
+            if width != x.shape[1] and width <= MAX_KERNEL_WIDTH:
+                xp = torch.empty((x.shape[0], width), dtype=x.dtype, device=x.device)
+                eng.prep_rows(x, xp, False)
+                x = xp
+            self._x = _padded(x)
+        else:
+            if metric == "cosine":
+                _normalize_(x)
+            self._x = _padded(x) if on_gpu else x
 
     # -- basics -------------------------------------------------------------
     def __len__(self) -> int:
@@ -98,6 +111,13 @@ class Index:
         if q.dim() != 2 or q.shape[1] != self.dim:
             raise ValueError(f"queries must be [b, {self.dim}]")
         q = q.to(self.device, self._x.dtype).contiguous()
+        width = self._x.shape[1]
+        if (self._use_kernels and width <= MAX_KERNEL_WIDTH and q.shape[0] > 0
+                and (self.metric == "cosine" or width != q.shape[1])):
+            # normalise (cosine) + zero-pad in one HIP pass into a new tensor
+            out = torch.empty((q.shape[0], width), dtype=q.dtype, device=q.device)
+            _ext.load().prep_rows(q, out, self.metric == "cosine")
+            return out
         if self.metric == "cosine":
             q = _normalize_(q.clone())
         return _padded(q) if self.device.type == "cuda" else q

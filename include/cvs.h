@@ -121,6 +121,20 @@ int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, i
                           int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,
                           int device, void* stream, void* const* marks);
 
+/*
+ * Row preparation, one pass: dst[r, 0:d] = src[r, 0:d], divided by
+ * max(||src[r, 0:d]||_2, 1e-12) (fp32 arithmetic, rounded once to fp16) when
+ * normalize != 0, and dst[r, d:dst_width] = 0.  Rows are fp16; src rows are
+ * src_stride elements apart, dst rows dst_width apart (d <= dst_width <= 1536).
+ * src == dst (in place) is allowed when src_stride == dst_width; other
+ * overlaps are not.  Replaces the torch sequences of index.py:35-41
+ * (_normalize_) and index.py:27-32 (_pad_width) used for cosine queries on
+ * every search (index.py:89-98) and for the corpus at construction
+ * (index.py:56-78).
+ */
+int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_stride, int64_t dst_width,
+                  int normalize, int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,8 @@ Contents, each restating one reference function (file:line into the reference):
   (fp32 ``q @ x.T`` + ``torch.topk``), used as a CPU baseline.
 * ``numpy_search``       - ``bench/bench_baselines.py:45-50`` (matmul +
   argpartition + argsort), used as a CPU baseline.
+* ``normalize_rows``     - ``index.py:35-41`` + ``index.py:27-32`` (cosine
+  normalisation and zero-padding of fp16 rows).
 * ``check_exact``        - the acceptance rule of ``tests/test_search.py:21-44``
   plus the id-parity rule (ids identical except inside the near-tie band of the
   k-th score).
@@ -173,6 +175,25 @@ def numpy_search(q: np.ndarray, x: np.ndarray, k: int):
     pv = np.take_along_axis(s, part, 1)
     order = np.argsort(-pv, axis=1)
     return np.take_along_axis(pv, order, 1), np.take_along_axis(part, order, 1)
+
+
+def normalize_rows(x, width: int | None = None, normalize: bool = True) -> np.ndarray:
+    """Restates ``index.py:35-41`` (``_normalize_``: fp16 rows to fp32, divide by
+    the L2 norm clamped at 1e-12, round to fp16) and ``index.py:27-32``
+    (``_pad_width``: zero columns up to ``width``).  The norm is accumulated in
+    float64 and rounded once to fp32 (any fp32 summation order is within its own
+    rounding error of it), so a GPU result may differ from this by one fp16 ulp
+    where the quotient sits at an fp16 rounding boundary."""
+    x16 = _as_half(x)
+    n, d = x16.shape
+    width = d if width is None else int(width)
+    f = x16.astype(np.float32)
+    if normalize:
+        nrm = np.sqrt((f.astype(np.float64) ** 2).sum(axis=1)).astype(np.float32)
+        f = f / np.maximum(nrm, np.float32(1e-12))[:, None]
+    out = np.zeros((n, width), dtype=np.float16)
+    out[:, :d] = f.astype(np.float16)
+    return out
 
 
 class ParityError(AssertionError):

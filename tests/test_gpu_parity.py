@@ -349,3 +349,75 @@ def test_baseline_configs_on_query_subset(eng, name):
     oracle.check_exact(qc, xc, k, v[sel].cpu(), ii[sel])
     del x, index
     torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------- row preparation
+
+
+def within_one_ulp(a16, b16):
+    """|a - b| <= one fp16 ulp at the larger of the two magnitudes (a quotient
+    just past a rounding midpoint may round either way between fp32 sums)."""
+    a, b = a16.astype(np.float32), b16.astype(np.float32)
+    ulp = np.maximum(np.abs(np.spacing(a16)), np.abs(np.spacing(b16))).astype(np.float32)
+    return np.abs(a - b) <= ulp
+
+
+@pytest.mark.parametrize("n,d,width", [(1, 1, 64), (1000, 100, 128), (4097, 384, 384), (513, 768, 768),
+                                       (77, 1536, 1536), (300, 700, 704)])
+def test_prep_rows_matches_oracle(eng, n, d, width):
+    """cvs_prep_rows (cosine normalisation + zero padding, index.py:27-41) within
+    one fp16 ulp of the oracle; pass-through and padding bit-exact; in place."""
+    say(f"prep_rows n={n} d={d} width={width}")
+    g = torch.Generator().manual_seed(n + d)
+    x = (torch.randn(n, d, generator=g) * torch.rand(n, 1, generator=g) * 10).half()
+    x[0] = 0  # a zero row stays zero
+    src = x.cuda()
+    out = torch.full((n, width), float("nan"), dtype=torch.float16, device="cuda")
+    eng.prep_rows(src, out, True)
+    copy = torch.full((n, width), float("nan"), dtype=torch.float16, device="cuda")
+    eng.prep_rows(src, copy, False)
+    torch.cuda.synchronize()
+    want = oracle.normalize_rows(x.numpy(), width=width)
+    got = out.cpu().numpy()
+    assert np.all(within_one_ulp(got, want))
+    assert not got[:, d:].any() and not got[0].any()
+    c = copy.cpu().numpy()
+    np.testing.assert_array_equal(c[:, :d], x.numpy())
+    assert not c[:, d:].any()
+    if width == d:  # in place
+        inplace = x.cuda()
+        eng.prep_rows(inplace, inplace, True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(inplace.cpu().numpy(), got)
+
+
+def test_prep_rows_errors(eng):
+    x = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="destination width"):
+        eng.prep_rows(x, torch.zeros(4, 32, dtype=torch.float16, device="cuda"), True)
+    with pytest.raises(RuntimeError, match="row width"):
+        eng.prep_rows(torch.zeros(4, 2000, dtype=torch.float16, device="cuda"),
+                      torch.zeros(4, 2048, dtype=torch.float16, device="cuda"), True)
+    with pytest.raises(RuntimeError, match="fp16 CUDA"):
+        eng.prep_rows(x.float(), x, True)
+
+
+def test_cosine_index_uses_the_prep_kernel_and_stays_exact(eng):
+    """Index(metric="cosine") normalises the corpus (in place, like the reference
+    with copy=False) and each query batch with cvs_prep_rows; search stays exact
+    against the stored rows, and a width that is not a multiple of 64 is padded."""
+    say("cosine index prep")
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(20000, 200, generator=g) * 3).half()
+    q = (torch.randn(40, 200, generator=g) * 5).half()
+    xd = x.cuda()
+    index = Index(xd, metric="cosine", copy=False)
+    assert index._x.shape == (20000, 256)
+    want = oracle.normalize_rows(x.numpy())
+    stored = index.embeddings.cpu().numpy()
+    assert np.all(within_one_ulp(stored, want))
+    np.testing.assert_array_equal(xd.cpu().numpy(), stored)  # caller's tensor normalised in place
+    v, i = index.search(q.cuda(), 10)
+    qn = index._prep_queries(q.cuda())
+    assert qn.shape == (40, 256) and not qn[:, 200:].any()
+    oracle.check_exact(qn[:, :200], index.embeddings, 10, v.cpu().numpy(), i.cpu().numpy())

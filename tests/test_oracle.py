@@ -158,3 +158,43 @@ def test_check_exact_accepts_oracle_and_rejects_planted_mistakes():
         oracle.check_exact(q, x, k, dv, dup)         # duplicate ids
     with pytest.raises(oracle.ParityError):
         oracle.check_exact(q, x, k - 1, v[:, :k - 1], i[:, 1:])  # best id missing
+
+
+# --------------------------------------------------------------------------- row preparation
+
+
+def test_normalize_rows_closed_forms():
+    """Pins oracle.normalize_rows: unit rows are fixed points, a zero row stays
+    zero (the 1e-12 clamp), power-of-two scalings normalise to the same row,
+    padding columns are zero, and the pass-through copies bit-exactly."""
+    e = np.zeros((3, 5), dtype=np.float16)
+    e[0, 0] = 1
+    e[1, :2] = [0.6, 0.8]           # |.| = 1 up to fp16 rounding of 0.6, 0.8
+    got = oracle.normalize_rows(e, width=64)
+    assert got.shape == (3, 64) and not got[:, 5:].any()
+    assert got[0, 0] == 1 and not got[0, 1:].any()
+    assert not got[2].any()         # zero row: divided by the clamp, stays 0
+    np.testing.assert_allclose(got[1, :2].astype(np.float32), [0.6, 0.8], atol=1e-3)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((50, 100)).astype(np.float16)
+    a = oracle.normalize_rows(x)
+    b = oracle.normalize_rows((x.astype(np.float32) * 8).astype(np.float16))
+    np.testing.assert_array_equal(a, b)
+    norms = np.linalg.norm(a.astype(np.float64), axis=1)
+    np.testing.assert_allclose(norms, 1.0, atol=2e-3)
+    np.testing.assert_array_equal(oracle.normalize_rows(x, width=128, normalize=False)[:, :100], x)
+
+
+def test_normalize_rows_agrees_with_the_torch_restatement():
+    """The package's torch path (index.py:35-41 restated with torch ops) and the
+    oracle agree within one fp16 ulp."""
+    import torch
+
+    from cuda_vector_search.index import _normalize_
+
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((200, 384)) * rng.uniform(0.1, 10, (200, 1))).astype(np.float16)
+    t = _normalize_(torch.from_numpy(x.copy())).numpy()
+    o = oracle.normalize_rows(x)
+    ulp = np.maximum(np.abs(np.spacing(o)), np.abs(np.spacing(t))).astype(np.float32)
+    assert np.all(np.abs(t.astype(np.float32) - o.astype(np.float32)) <= ulp)
