@@ -547,6 +547,34 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   return CVS_OK;
 }
 
+int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, float* out_v, void* out_i,
+                  int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  if (k < 1 || k > kSelectMaxK) return fail(CVS_ERR_INVALID, "topk_rows supports 1 <= k <= %d", kSelectMaxK);
+  if (k > n) return fail(CVS_ERR_INVALID, "k must not exceed the row length");
+  if (n >= INT_MAX) return fail(CVS_ERR_INVALID, "rows must have fewer than 2^31 columns");
+  if (nq < 0 || nq >= INT_MAX) return fail(CVS_ERR_INVALID, "too many rows");
+  if (nq == 0) return CVS_OK;
+  if (scores == nullptr || out_v == nullptr || out_i == nullptr) return fail(CVS_ERR_INVALID, "pointers must not be null");
+  if (reinterpret_cast<uintptr_t>(scores) % 4 != 0) return fail(CVS_ERR_INVALID, "scores must be 4-byte aligned");
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  SelectArgs sa{};
+  sa.lv = scores;  // one list per row holding all n scores; the id is the column
+  sa.nlists = 1;
+  sa.cap = (int)n;
+  sa.k = (int)k;
+  sa.out_v = out_v;
+  sa.out_i = out_i;
+  sa.ids64 = (flags & CVS_FLAG_IDS_INT64) ? 1 : 0;
+  hipError_t e = launch_select(0, sa, (int)nq, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "select launch");
+  return CVS_OK;
+}
+
 int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_stride, int64_t dst_width,
                   int normalize, int device, void* stream) {
   DevInfo di;

@@ -116,5 +116,6 @@ bool scan_cfg_available(const ScanCfg& cfg, int mode);
 
 constexpr int kSelectMaxLists = 8192;
 constexpr int kMaxCap = 512;  // largest candidate-list capacity (k <= 256)
+constexpr int kSelectMaxK = 1024;  // largest k of the select kernel (row top-k of a score matrix)
 
 }  // namespace cvs

@@ -12,7 +12,9 @@
 // like the reference's.
 //
 // Threshold mode returns only the score of the k-th best key (used to turn the
-// sampling pre-pass's unit maxima into per-query thresholds).
+// sampling pre-pass's unit maxima into per-query thresholds).  With one list
+// per query holding a whole score row it is also the row top-k of a score
+// matrix (k up to 1024: the large-k path).
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
 }  // namespace
 
 hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s) {
-  if (a.nlists < 1 || a.nlists > kSelectMaxLists || a.k < 1 || a.k > 256) return hipErrorInvalidValue;
+  if (a.nlists < 1 || a.nlists > kSelectMaxLists || a.k < 1 || a.k > kSelectMaxK) return hipErrorInvalidValue;
   if (tau_mode)
     hipLaunchKernelGGL(select_kernel<1>, dim3(nq), dim3(kBlock), 0, s, a);
   else

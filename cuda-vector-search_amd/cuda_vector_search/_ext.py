@@ -66,6 +66,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.cvs_fused_topk_timed.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                          vp, vp, ctypes.POINTER(i64), i32, vp,
                                          ctypes.POINTER(ctypes.c_float)]
+    lib.cvs_topk_rows.restype = i32
+    lib.cvs_topk_rows.argtypes = [vp, i64, i64, i64, i32, vp, vp, i32, vp]
     lib.cvs_prep_rows.restype = i32
     lib.cvs_prep_rows.argtypes = [vp, vp, i64, i64, i64, i64, i32, i32, vp]
     lib.cvs_fused_topk_marked.restype = i32
@@ -145,6 +147,24 @@ class Engine:
                                     1 if normalize else 0, src.device.index, self._stream(src.device))
         if rc != 0:
             raise self._error(rc)
+
+    def topk_rows(self, s, k: int, flags: int = 0):
+        """Exact top-k (values desc, column asc) of each row of a fp32 CUDA
+        matrix; ids int32 (int64 with FLAG_IDS_INT64)."""
+        import torch
+
+        if not (isinstance(s, torch.Tensor) and s.is_cuda and s.dtype == torch.float32 and s.dim() == 2
+                and s.is_contiguous()):
+            raise RuntimeError("topk_rows needs a contiguous 2-D float32 CUDA tensor")
+        nq, n = s.shape
+        k = int(k)
+        v = torch.empty((nq, k), dtype=torch.float32, device=s.device)
+        i = torch.empty((nq, k), dtype=torch.int64 if flags & FLAG_IDS_INT64 else torch.int32, device=s.device)
+        rc = self.lib.cvs_topk_rows(s.data_ptr(), nq, n, k, flags, v.data_ptr(), i.data_ptr(), s.device.index,
+                                    self._stream(s.device))
+        if rc != 0:
+            raise self._error(rc)
+        return v, i
 
     # -- reference API -------------------------------------------------------
     def scores(self, q, x, out_fp32: bool = True):

@@ -21,6 +21,8 @@ from .reference import torch_topk
 
 PAD = 64            # widths are zero-padded to a multiple of this (the MFMA depth step x 2)
 MAX_FUSED_K = 256   # largest k of the fused path
+MAX_EXACT_K = 1024  # largest k of the exact large-k path (score matrix + row top-k)
+_SCORE_BLOCK_BYTES = 1 << 31  # fp32 score rows computed per block on the large-k path
 MAX_KERNEL_WIDTH = 1536  # widest (padded) rows the gfx950 kernels accept
 _NORM_CHUNK = 1 << 18
 
@@ -130,7 +132,8 @@ class Index:
             "fused"   - gfx950 engine: MFMA scores + threshold filter + exact select (k <= 256)
             "twopass" - gfx950 score kernel writes the fp16 matrix, then torch.topk
             "torch"   - torch matmul + torch.topk
-            "auto"    - fused when possible, else torch
+            "auto"    - fused for k <= 256; exact fp32 scores + row top-k for k <= 1024;
+                        else torch
         """
         if method not in METHODS:
             raise ValueError(f"method must be one of {METHODS}")
@@ -140,8 +143,13 @@ class Index:
         k = min(k, len(self))
         q = self._prep_queries(queries)
         if method == "auto":
-            fits = k <= MAX_FUSED_K and self._x.shape[1] <= MAX_KERNEL_WIDTH
-            method = "fused" if (self._use_kernels and fits) else "torch"
+            width_ok = self._use_kernels and self._x.shape[1] <= MAX_KERNEL_WIDTH
+            if width_ok and k <= MAX_FUSED_K:
+                method = "fused"
+            elif width_ok and k <= MAX_EXACT_K:
+                return self._search_large_k(q, k)
+            else:
+                method = "torch"
         if method in ("fused", "twopass") and not self._use_kernels:
             raise RuntimeError(f"method={method!r} needs an AMD Instinct MI355X (gfx950) GPU")
         if method == "fused":
@@ -155,6 +163,28 @@ class Index:
             v, i = torch.topk(s, k, dim=1)
             return v.float(), i
         return torch_topk(q, self._x, k)
+
+    def _search_large_k(self, q: torch.Tensor, k: int):
+        """Exact top-k for MAX_FUSED_K < k <= MAX_EXACT_K on the GPU: fp32 score
+        rows from the score kernel, then the exact row top-k, in query blocks of
+        at most 2 GB of scores.  (The reference sends k > 256 to torch with fp16
+        scores, index.py:118.)"""
+        eng = _ext.load()
+        n = len(self)
+        if q.shape[0] == 0:
+            return (torch.empty((0, k), dtype=torch.float32, device=q.device),
+                    torch.empty((0, k), dtype=torch.int64, device=q.device))
+        rows = max(1, _SCORE_BLOCK_BYTES // (4 * n))
+        vs, ids = [], []
+        for lo in range(0, q.shape[0], rows):
+            s = eng.scores(q[lo:lo + rows], self._x, True)
+            v, i = eng.topk_rows(s, k, flags=_ext.FLAG_IDS_INT64)
+            vs.append(v)
+            ids.append(i)
+            del s
+        if len(vs) == 1:
+            return vs[0], ids[0]
+        return torch.cat(vs), torch.cat(ids)
 
     def scores(self, queries, fp32: bool = True) -> torch.Tensor:
         """Full ``[b, n]`` score matrix (gfx950 score kernel on a GPU index)."""

@@ -122,6 +122,18 @@ int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, i
                           int device, void* stream, void* const* marks);
 
 /*
+ * Exact top-k of each row of an fp32 matrix scores[nq, n] (row-major): the k
+ * largest values of each row with their column indices, sorted by value
+ * descending then index ascending (the fused path's order).  1 <= k <= 1024,
+ * k <= n.  out_v is [nq, k] fp32, out_i [nq, k] int32 (int64 with
+ * CVS_FLAG_IDS_INT64; other flag bits are ignored).  With cvs_scores this is
+ * the exact large-k search that the reference leaves to torch (fp16 matmul +
+ * torch.topk, index.py:118 / reference.py:8-15) for k > 256.
+ */
+int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, float* out_v, void* out_i,
+                  int device, void* stream);
+
+/*
  * Row preparation, one pass: dst[r, 0:d] = src[r, 0:d], divided by
  * max(||src[r, 0:d]||_2, 1e-12) (fp32 arithmetic, rounded once to fp16) when
  * normalize != 0, and dst[r, d:dst_width] = 0.  Rows are fp16; src rows are

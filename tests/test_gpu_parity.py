@@ -421,3 +421,45 @@ def test_cosine_index_uses_the_prep_kernel_and_stays_exact(eng):
     qn = index._prep_queries(q.cuda())
     assert qn.shape == (40, 256) and not qn[:, 200:].any()
     oracle.check_exact(qn[:, :200], index.embeddings, 10, v.cpu().numpy(), i.cpu().numpy())
+
+
+# --------------------------------------------------------------------------- large k
+
+
+@pytest.mark.parametrize("nq,n,k", [(3, 5000, 1), (7, 20000, 300), (2, 3000, 1024), (5, 1024, 1024)])
+def test_topk_rows_matches_sorted_rows(eng, nq, n, k):
+    """cvs_topk_rows equals a stable sort of each row (value desc, column asc),
+    including exact ties (the matrix holds repeated values)."""
+    say(f"topk_rows nq={nq} n={n} k={k}")
+    g = torch.Generator().manual_seed(n + k)
+    s = torch.randint(-500, 500, (nq, n), generator=g).float() / 64  # many exact ties
+    v, i = eng.topk_rows(s.cuda(), k)
+    v64, i64 = eng.topk_rows(s.cuda(), k, flags=_ext.FLAG_IDS_INT64)
+    torch.cuda.synchronize()
+    sn = s.numpy()
+    order = np.lexsort((np.broadcast_to(np.arange(n), sn.shape), -sn), axis=1)[:, :k]
+    np.testing.assert_array_equal(i.cpu().numpy(), order)
+    np.testing.assert_array_equal(v.cpu().numpy(), np.take_along_axis(sn, order, axis=1))
+    assert i64.dtype == torch.int64 and torch.equal(i64.cpu(), i.cpu().long()) and torch.equal(v64, v)
+
+
+def test_topk_rows_errors(eng):
+    s = torch.zeros(2, 100, device="cuda")
+    with pytest.raises(RuntimeError, match="1 <= k <= 1024"):
+        eng.topk_rows(s, 1025)
+    with pytest.raises(RuntimeError, match="must not exceed"):
+        eng.topk_rows(s, 101)
+    with pytest.raises(RuntimeError, match="float32"):
+        eng.topk_rows(s.half(), 5)
+
+
+@pytest.mark.parametrize("b,k", [(5, 300), (40, 1024), (1, 700)])
+def test_large_k_search_is_exact(eng, b, k):
+    """Index.search with 256 < k <= 1024 runs the score kernel + row top-k on the
+    GPU (the reference falls back to torch fp16 scores) and is exact."""
+    say(f"large-k search b={b} k={k}")
+    x, q = make(20000, 128, b, seed=k)
+    index = Index(x.cuda(), metric="ip")
+    v, i = index.search(q.cuda(), k)
+    assert v.dtype == torch.float32 and i.dtype == torch.int64 and v.shape == (b, k)
+    oracle.check_exact(q, x, k, v.cpu().numpy(), i.cpu().numpy())
