@@ -547,30 +547,93 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   return CVS_OK;
 }
 
-int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, float* out_v, void* out_i,
-                  int device, void* stream) {
-  DevInfo di;
-  int rc = dev_info(device, &di);
-  if (rc != CVS_OK) return rc;
-  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+namespace {
+
+// Chunks per row for cvs_topk_rows: enough workgroups to keep ~4 per CU busy,
+// chunks of at least max(4096, 2k) columns, at most kSelectMaxLists of them.
+int64_t rowtopk_chunks(int64_t nq, int64_t n, int64_t k, int cus) {
+  const int64_t want = ceil_div(4 * (int64_t)cus, std::max<int64_t>(nq, 1));
+  const int64_t most = std::max<int64_t>(1, n / std::max<int64_t>(4096, 2 * k));
+  int64_t c = std::max<int64_t>(1, std::min<int64_t>({want, most, (int64_t)kSelectMaxLists}));
+  const int64_t len = ceil_div(n, c);
+  return ceil_div(n, len);
+}
+
+int check_topk_rows(int64_t nq, int64_t n, int64_t k) {
   if (k < 1 || k > kSelectMaxK) return fail(CVS_ERR_INVALID, "topk_rows supports 1 <= k <= %d", kSelectMaxK);
   if (k > n) return fail(CVS_ERR_INVALID, "k must not exceed the row length");
   if (n >= INT_MAX) return fail(CVS_ERR_INVALID, "rows must have fewer than 2^31 columns");
   if (nq < 0 || nq >= INT_MAX) return fail(CVS_ERR_INVALID, "too many rows");
+  return CVS_OK;
+}
+
+}  // namespace
+
+int cvs_topk_rows_plan(int64_t nq, int64_t n, int64_t k, int device, int64_t* workspace_bytes) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  rc = check_topk_rows(nq, n, k);
+  if (rc != CVS_OK) return rc;
+  const int64_t c = rowtopk_chunks(nq, n, k, di.cus);
+  if (nq * c >= INT_MAX) return fail(CVS_ERR_INVALID, "too many rows");
+  if (workspace_bytes) *workspace_bytes = c > 1 ? align_up(nq * c * k * 4, 256) * 2 : 0;
+  return CVS_OK;
+}
+
+int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, void* workspace,
+                  int64_t workspace_bytes, float* out_v, void* out_i, int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  rc = check_topk_rows(nq, n, k);
+  if (rc != CVS_OK) return rc;
   if (nq == 0) return CVS_OK;
   if (scores == nullptr || out_v == nullptr || out_i == nullptr) return fail(CVS_ERR_INVALID, "pointers must not be null");
   if (reinterpret_cast<uintptr_t>(scores) % 4 != 0) return fail(CVS_ERR_INVALID, "scores must be 4-byte aligned");
+  const int64_t c = rowtopk_chunks(nq, n, k, di.cus);
+  if (nq * c >= INT_MAX) return fail(CVS_ERR_INVALID, "too many rows");
+  const int64_t part = align_up(nq * c * k * 4, 256);
+  if (c > 1) {
+    if (workspace == nullptr || workspace_bytes < 2 * part)
+      return fail(CVS_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)(2 * part),
+                  (long long)workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(CVS_ERR_INVALID, "workspace must be 256-byte aligned");
+  }
   DeviceGuard guard(device);
   if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
-  SelectArgs sa{};
-  sa.lv = scores;  // one list per row holding all n scores; the id is the column
-  sa.nlists = 1;
-  sa.cap = (int)n;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int ids64 = (flags & CVS_FLAG_IDS_INT64) ? 1 : 0;
+  RowTopkArgs r{};
+  r.scores = scores;
+  r.n = n;
+  r.len = ceil_div(n, c);
+  r.chunks = (int)c;
+  r.k = (int)k;
+  if (c == 1) {  // one chunk per row: the first stage is the answer
+    r.out_v = out_v;
+    r.out_i = out_i;
+    r.ids64 = ids64;
+    hipError_t e = launch_rowtopk(r, (int)nq, s);
+    return e == hipSuccess ? CVS_OK : hip_fail(e, "row top-k launch");
+  }
+  char* ws = static_cast<char*>(workspace);
+  r.out_v = reinterpret_cast<float*>(ws);
+  r.out_i = ws + part;
+  r.ids64 = 0;
+  hipError_t e = launch_rowtopk(r, (int)(nq * c), s);
+  if (e != hipSuccess) return hip_fail(e, "row top-k launch");
+  SelectArgs sa{};  // second stage: merge the c sorted chunk lists of each row
+  sa.lv = r.out_v;
+  sa.li = reinterpret_cast<const int*>(r.out_i);
+  sa.nlists = (int)c;
+  sa.cap = (int)k;
   sa.k = (int)k;
   sa.out_v = out_v;
   sa.out_i = out_i;
-  sa.ids64 = (flags & CVS_FLAG_IDS_INT64) ? 1 : 0;
-  hipError_t e = launch_select(0, sa, (int)nq, reinterpret_cast<hipStream_t>(stream));
+  sa.ids64 = ids64;
+  e = launch_select(0, sa, (int)nq, s);
   if (e != hipSuccess) return hip_fail(e, "select launch");
   return CVS_OK;
 }

@@ -68,6 +68,18 @@ struct GemvArgs {
   int mode;           // kAppend or kMax
 };
 
+// Row top-k, first stage: one workgroup per (row, chunk of `len` columns).
+struct RowTopkArgs {
+  const float* scores;  // [rows, n] fp32
+  int64_t n;
+  int64_t len;          // columns per chunk
+  int chunks;           // chunks per row (ceil(n / len))
+  int k;
+  float* out_v;         // [rows * chunks, k]
+  void* out_i;          // [rows * chunks, k] int32 column ids (int64 when ids64)
+  int ids64;
+};
+
 // Row preparation: dst[r, :d] = src[r, :d] (scaled to unit L2 norm when
 // normalize), dst[r, d:width] = 0.
 struct PrepArgs {
@@ -111,6 +123,7 @@ hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid
 hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
 hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
+hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s);
 
 bool scan_cfg_available(const ScanCfg& cfg, int mode);
 

@@ -26,9 +26,10 @@ constexpr int kBuf = 4096;    // LDS key buffer
 constexpr int kBatch = 2048;  // candidates gathered per round
 constexpr int kWaves = kBlock / kWave;
 
-struct SelShared {
+template <int MAXL>
+struct SelSharedT {
   uint64_t keys[kBuf];
-  int pre[kSelectMaxLists + 1];
+  int pre[MAXL + 1];
   int part[kBlock];
   int hist[kWaves][256];
   int nbuf;
@@ -38,10 +39,13 @@ struct SelShared {
   int stop;
   uint64_t thr_key;
 };
+typedef SelSharedT<kSelectMaxLists> SelShared;
+typedef SelSharedT<1> RowShared;  // no list offsets: ~38 KB, several workgroups per CU
 
 // Cuts keys[0..nb) down to its k largest keys (nb > k), in place and in any
 // order, and returns the k-th largest key.  Whole block.
-__device__ uint64_t block_keep_top(SelShared& S, int nb, int k) {
+template <class SH>
+__device__ uint64_t block_keep_top(SH& S, int nb, int k) {
   const int tid = threadIdx.x;
   const int w = tid / kWave;
   const int lane = tid % kWave;
@@ -237,7 +241,91 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
 }
 
+// Exact top-k of one chunk of one score row: workgroup b takes row b / chunks,
+// columns [c*len, min((c+1)*len, n)) with c = b % chunks, and writes its k
+// best (value, column) sorted to out[b].  Each thread loads kRowU values per
+// round with all loads in flight, then appends the ones above the running k-th
+// best key in kBatch-sized steps (wave-aggregated LDS appends).
+constexpr int kRowU = 32;
+
+__global__ __launch_bounds__(kBlock) void rowtopk_kernel(RowTopkArgs a) {
+  __shared__ RowShared S;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int b = blockIdx.x;
+  const int q = b / a.chunks;
+  const int c = b % a.chunks;
+  const int64_t start = (int64_t)c * a.len;
+  const int cnt = (int)min<int64_t>(a.len, a.n - start);
+  const float* src = a.scores + (int64_t)q * a.n + start;
+  const int k = a.k;
+  if (tid == 0) {
+    S.nbuf = 0;
+    S.thr_key = 0ull;
+  }
+  __syncthreads();
+  constexpr int kRound = kRowU * kBlock;
+  for (int base = 0; base < cnt; base += kRound) {
+    float val[kRowU];
+#pragma unroll
+    for (int u = 0; u < kRowU; ++u) {  // coalesced; a slot past the end re-reads column 0
+      const int gi = base + u * kBlock + tid;
+      val[u] = src[gi < cnt ? gi : 0];
+    }
+#pragma unroll
+    for (int sub = 0; sub < kRowU / (kBatch / kBlock); ++sub) {
+      const uint64_t t = S.thr_key;
+#pragma unroll
+      for (int j = 0; j < kBatch / kBlock; ++j) {
+        const int u = sub * (kBatch / kBlock) + j;
+        const int gi = base + u * kBlock + tid;
+        const uint64_t key = make_key(val[u], (int)(start + gi));
+        const bool pass = gi < cnt && key > t;
+        const uint64_t mk = __ballot(pass);
+        int pos = 0;
+        if (lane == 0 && mk) pos = atomicAdd(&S.nbuf, __popcll(mk));
+        pos = __shfl(pos, 0);
+        if (pass) S.keys[pos + lanes_below(mk)] = key;
+      }
+      __syncthreads();
+      const int nb = S.nbuf;
+      const bool last = base + (sub + 1) * kBatch >= cnt;
+      if (nb > kBuf - kBatch || (last && nb > k)) {
+        const uint64_t kth = block_keep_top(S, nb, k);
+        if (tid == 0) {
+          S.nbuf = k;
+          S.thr_key = kth;
+        }
+        __syncthreads();
+      }
+      if (last) break;
+    }
+  }
+  const int nb = min(S.nbuf, k);
+  int N = 2;
+  while (N < nb) N <<= 1;
+  for (int i = nb + tid; i < N; i += kBlock) S.keys[i] = 0ull;
+  __syncthreads();
+  block_sort_desc(S.keys, N);
+  for (int r = tid; r < k; r += kBlock) {
+    const bool ok = r < nb;
+    const int64_t o = (int64_t)b * k + r;
+    a.out_v[o] = ok ? key_score(S.keys[r]) : -__builtin_inff();
+    const int id = ok ? key_id(S.keys[r]) : -1;
+    if (a.ids64)
+      ((int64_t*)a.out_i)[o] = id;
+    else
+      ((int*)a.out_i)[o] = id;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s) {
+  if (a.k < 1 || a.k > kSelectMaxK || a.chunks < 1 || a.len < 1 || blocks < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rowtopk_kernel, dim3(blocks), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s) {
   if (a.nlists < 1 || a.nlists > kSelectMaxLists || a.k < 1 || a.k > kSelectMaxK) return hipErrorInvalidValue;

@@ -67,7 +67,9 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
                                          vp, vp, ctypes.POINTER(i64), i32, vp,
                                          ctypes.POINTER(ctypes.c_float)]
     lib.cvs_topk_rows.restype = i32
-    lib.cvs_topk_rows.argtypes = [vp, i64, i64, i64, i32, vp, vp, i32, vp]
+    lib.cvs_topk_rows.argtypes = [vp, i64, i64, i64, i32, vp, i64, vp, vp, i32, vp]
+    lib.cvs_topk_rows_plan.restype = i32
+    lib.cvs_topk_rows_plan.argtypes = [i64, i64, i64, i32, ctypes.POINTER(i64)]
     lib.cvs_prep_rows.restype = i32
     lib.cvs_prep_rows.argtypes = [vp, vp, i64, i64, i64, i64, i32, i32, vp]
     lib.cvs_fused_topk_marked.restype = i32
@@ -158,10 +160,15 @@ class Engine:
             raise RuntimeError("topk_rows needs a contiguous 2-D float32 CUDA tensor")
         nq, n = s.shape
         k = int(k)
+        ws_bytes = ctypes.c_int64(0)
+        rc = self.lib.cvs_topk_rows_plan(nq, n, k, s.device.index, ctypes.byref(ws_bytes))
+        if rc != 0:
+            raise self._error(rc)
         v = torch.empty((nq, k), dtype=torch.float32, device=s.device)
         i = torch.empty((nq, k), dtype=torch.int64 if flags & FLAG_IDS_INT64 else torch.int32, device=s.device)
-        rc = self.lib.cvs_topk_rows(s.data_ptr(), nq, n, k, flags, v.data_ptr(), i.data_ptr(), s.device.index,
-                                    self._stream(s.device))
+        ws = torch.empty(max(int(ws_bytes.value), 256), dtype=torch.uint8, device=s.device)
+        rc = self.lib.cvs_topk_rows(s.data_ptr(), nq, n, k, flags, ws.data_ptr(), ws.numel(), v.data_ptr(),
+                                    i.data_ptr(), s.device.index, self._stream(s.device))
         if rc != 0:
             raise self._error(rc)
         return v, i

@@ -126,12 +126,18 @@ int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, i
  * largest values of each row with their column indices, sorted by value
  * descending then index ascending (the fused path's order).  1 <= k <= 1024,
  * k <= n.  out_v is [nq, k] fp32, out_i [nq, k] int32 (int64 with
- * CVS_FLAG_IDS_INT64; other flag bits are ignored).  With cvs_scores this is
+ * CVS_FLAG_IDS_INT64; other flag bits are ignored).  Rows are split into
+ * chunks whose k best are merged by the select kernel; `workspace` holds the
+ * chunk results (size from cvs_topk_rows_plan).  With cvs_scores this is
  * the exact large-k search that the reference leaves to torch (fp16 matmul +
  * torch.topk, index.py:118 / reference.py:8-15) for k > 256.
  */
-int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, float* out_v, void* out_i,
-                  int device, void* stream);
+int cvs_topk_rows(const float* scores, int64_t nq, int64_t n, int64_t k, int flags, void* workspace,
+                  int64_t workspace_bytes, float* out_v, void* out_i, int device, void* stream);
+
+/* Workspace bytes cvs_topk_rows needs for these sizes (0 when each row is
+ * handled by one workgroup); 256-byte aligned, no initialisation needed. */
+int cvs_topk_rows_plan(int64_t nq, int64_t n, int64_t k, int device, int64_t* workspace_bytes);
 
 /*
  * Row preparation, one pass: dst[r, 0:d] = src[r, 0:d], divided by

@@ -426,7 +426,8 @@ def test_cosine_index_uses_the_prep_kernel_and_stays_exact(eng):
 # --------------------------------------------------------------------------- large k
 
 
-@pytest.mark.parametrize("nq,n,k", [(3, 5000, 1), (7, 20000, 300), (2, 3000, 1024), (5, 1024, 1024)])
+@pytest.mark.parametrize("nq,n,k", [(3, 5000, 1), (7, 20000, 300), (2, 3000, 1024), (5, 1024, 1024),
+                                    (2, 200000, 100), (1, 1 << 20, 1024)])
 def test_topk_rows_matches_sorted_rows(eng, nq, n, k):
     """cvs_topk_rows equals a stable sort of each row (value desc, column asc),
     including exact ties (the matrix holds repeated values)."""
