@@ -517,15 +517,26 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   if (rc != CVS_OK) return rc;
   if (nq == 0 || n == 0) return CVS_OK;
   if (out == nullptr) return fail(CVS_ERR_INVALID, "output pointer must not be null");
+  // Same query blocks and chunking as the fused plan: one workgroup per CU,
+  // chunks a multiple of the 8 XCDs when several query groups share them.
   ScanCfg cfg;
-  cfg_for(nq <= 16 ? 16 : 64, d, &cfg);
-  const int64_t bq = cfg.bq();
+  int64_t bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d > 384) ? 128 : 256;
+  while (!cfg_for(bq, d, &cfg)) bq >>= 1;
   const int64_t groups = ceil_div(nq, bq);
   const int64_t ntiles = ceil_div(n, cfg.tile_rows());
-  int64_t c = std::max<int64_t>(1, ceil_div(2 * (int64_t)di.cus, groups));
-  c = std::min<int64_t>({c, ntiles, 65535});
-  const int64_t tpc = ceil_div(ntiles, c);
-  c = ceil_div(ntiles, tpc);
+  const int64_t max_chunks = std::min<int64_t>(ntiles, 65535);
+  int64_t c = std::max<int64_t>(1, ceil_div(di.cus, groups));
+  c = std::min<int64_t>({c, std::max<int64_t>(1, ntiles / 2), max_chunks});
+  int64_t tpc;
+  int xcd_pair = 0;
+  if (groups > 1 && c >= 8) {
+    c = std::min<int64_t>(align_up(c, 8), (max_chunks / 8) * 8);
+    tpc = ceil_div(ntiles, c);
+    xcd_pair = 1;
+  } else {
+    tpc = ceil_div(ntiles, c);
+    c = ceil_div(ntiles, tpc);
+  }
   if (groups * c > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
 
   DeviceGuard guard(device);
@@ -540,6 +551,7 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   a.nchunks = (int)c;
   a.ntiles = ntiles;
   a.tpc = tpc;
+  a.xcd_pair = xcd_pair;
   a.out = out;
   hipError_t e = launch_scan(cfg, out_fp32 ? kStoreF32 : kStoreF16, a, (int)(groups * c),
                              reinterpret_cast<hipStream_t>(stream));

@@ -110,6 +110,11 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
   __shared__ int st_meta[APP ? NW : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
   __shared__ uint64_t sortbuf[APP ? NW * kMaxCap : 1];  // compaction scratch
+  // kStore*: each wave's [QW queries][RW rows] score tile, written out one query
+  // row at a time by consecutive lanes (coalesced); rows padded by 4 elements.
+  constexpr bool STORE = (MODE == kStoreF32 || MODE == kStoreF16);
+  constexpr int SROW = RW + 4;
+  __shared__ __attribute__((aligned(16))) float stg[STORE ? NW : 1][STORE ? QW * SROW : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -371,6 +376,16 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) ab[0][kk][rb] = ab[1][kk][rb];
     }
+    // The epilogue's first VALU reads of the accumulators can follow the
+    // tile's last MFMA within a few instructions (across the partial-tile
+    // branch).  Pad with 19 wait states (a 16-pass MFMA's result latency)
+    // after the last MFMA; the empty asm statements order every accumulator
+    // read after the padding.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2" : "+v"(acc[QB - 1][RB - 1]));
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) asm volatile("" : "+v"(acc[qb][rb]));
 
     // ---- epilogue: acc[qb][rb][e] = score(query qwave0 + MS*qb + col,
     //                                        row rowb + MS*rb + M::row(e))
@@ -393,18 +408,16 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
             if (rb * MS + M::row(e) >= left) v[rb * M::NE + e] = -__builtin_inff();
       }
 
-      if (MODE == kStoreF32 || MODE == kStoreF16) {
-        if (qi < a.nq) {
+      if (STORE) {  // into this wave's LDS tile: [query qb*MS + col][row rb*MS + 4kg + row(e)]
+        const int qo = (qb * MS + col) * SROW + 4 * kg;
 #pragma unroll
-          for (int j = 0; j < NV; ++j) {
-            const int64_t row = rowb + (j / M::NE) * MS + M::row(j % M::NE);
-            if (row < n) {
-              if (MODE == kStoreF32)
-                ((float*)a.out)[(int64_t)qi * n + row] = v[j];
-              else
-                ((_Float16*)a.out)[(int64_t)qi * n + row] = (_Float16)v[j];
-            }
-          }
+        for (int j = 0; j < NV; j += 4) {  // elements 4c..4c+3 are 4 consecutive rows
+          const int r = (j / M::NE) * MS + M::row(j % M::NE);
+          if (MODE == kStoreF32)
+            *(f32x4*)(&stg[w][qo + r]) = f32x4{v[j], v[j + 1], v[j + 2], v[j + 3]};
+          else
+            *(half4*)((_Float16*)stg[w] + qo + r) =
+                half4{(_Float16)v[j], (_Float16)v[j + 1], (_Float16)v[j + 2], (_Float16)v[j + 3]};
         }
       } else {
         if (MODE == kMax) {
@@ -442,6 +455,45 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
           }
         }
       }
+    }
+    if (STORE) {  // write the tile out: each query's RW rows by RW/4 consecutive lanes, 4 rows each
+      constexpr int LPQ = RW / 4;      // lanes per query
+      constexpr int QPI = kWave / LPQ; // queries per store instruction
+      static_assert(QW % QPI == 0, "store read-out shape");
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int r4 = 4 * (lane % LPQ);
+      const int64_t row = t * TR + rs * RW + r4;
+      // 16-byte (fp32) / 8-byte (fp16) stores need 4 | n (row starts aligned) and 4 whole rows
+      const bool vec = (n % 4 == 0) && (row + 4 <= n);
+#pragma unroll 4
+      for (int qq = lane / LPQ; qq < QW; qq += QPI) {
+        const int qi = qwave0 + qq;
+        if (qi < a.nq) {
+          const int so = qq * SROW + r4;
+          if (MODE == kStoreF32) {
+            const f32x4 x4 = *(const f32x4*)(&stg[w][so]);
+            float* o = (float*)a.out + (int64_t)qi * n + row;
+            if (vec) {
+              *(f32x4*)o = x4;
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (row + i < n) o[i] = x4[i];
+            }
+          } else {
+            const half4 x4 = *(const half4*)((const _Float16*)stg[w] + so);
+            _Float16* o = (_Float16*)a.out + (int64_t)qi * n + row;
+            if (vec) {
+              *(half4*)o = x4;
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (row + i < n) o[i] = x4[i];
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
   }
   if (APP && st_n > 0) flush();
@@ -484,10 +536,16 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
         hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     case kStoreF32:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+      if (full)
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+      else
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     case kStoreF16:
-      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+      if (full)
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+      else
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;

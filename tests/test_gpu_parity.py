@@ -72,7 +72,9 @@ def run_fused(eng, q, x, k, **kw):
 
 
 @pytest.mark.parametrize("nq,n,d", [(37, 3001, 192), (5, 1000, 64), (100, 2000, 768),
-                                    (3, 517, 1536), (16, 64, 384), (70, 130, 128)])
+                                    (3, 517, 1536), (16, 64, 384), (70, 130, 128),
+                                    (300, 20000, 384), (200, 9999, 768), (129, 4097, 256),
+                                    (257, 3, 64)])
 def test_scores_kernel_matches_oracle(eng, nq, n, d):
     say(f"scores nq={nq} n={n} d={d}")
     x, q = make(n, d, nq, seed=n + d)
