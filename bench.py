@@ -11,11 +11,14 @@ config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
 
 * value / ms_per_step: host-timed whole-batch throughput (queries/s) over K steps
   bracketed by device synchronisation;
-* roofline: the dominant kernel (the MFMA scan, or the GEMV at batch 1) timed
-  with HIP events that the library records on the stream it launches on, over
-  a second timed region of K back-to-back calls, against its algorithmic bytes
-  (corpus read once + queries) and the MI355X peaks (8 TB/s HBM; 2.5 PFLOP/s
-  dense fp16 MFMA also reported as mfma_frac).  ``traffic`` is the kernel's
+* roofline: the dominant kernel of the path ``Index.search`` takes (the fp16
+  MFMA scan / GEMV, or their int8 pre-filter forms over the int8 companion of
+  the corpus where "auto" picks it) timed with HIP events that the library
+  records on the stream it launches on, over a second timed region of K
+  back-to-back calls, against its algorithmic bytes (corpus read once +
+  queries, in the kernel's element type) and the MI355X peaks (8 TB/s HBM;
+  2.5 PFLOP/s dense fp16 / 5.0 POP/s int8 MFMA as mfma_frac).  Each config row
+  also times the other exact path on the same batch.  ``traffic`` is the kernel's
   measured HBM bytes per launch: two child runs of this script under
   ``rocprofv3 --pmc`` (FETCH_SIZE, then WRITE_SIZE), each scaled by what the
   same counter reads for a plain 1 GiB device copy in the same child;
@@ -44,6 +47,7 @@ for _p in (str(REPO), str(REPO / "cuda-vector-search_amd")):
 METRIC = "queries/sec at 1M×384 b256 k10; ms/batch + HBM GB/s at 4M×768 b1"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP16_PEAK = 2.5e15
+MFMA_INT8_PEAK = 5.0e15
 REF_T4_QPS_C2 = 13178.5  # reference fused kernel on a Tesla T4, C2
 
 
@@ -52,11 +56,18 @@ def log(*a):
 
 
 def kernel_bytes(n, d, b):
-    """Algorithmic HBM bytes of one scan/GEMV launch: corpus once + queries."""
+    """Algorithmic HBM bytes of one fp16 scan/GEMV launch: corpus once + queries."""
     return 2 * n * d + 2 * b * d
 
 
+def kernel_bytes_q8(n, dq, b):
+    """Algorithmic HBM bytes of one int8 scan/GEMV launch: int8 corpus once + int8 queries."""
+    return n * dq + b * dq
+
+
 def run_config(name, steps, warmup, eng, torch, synthetic, Index):
+    from cuda_vector_search.index import q8_row_bytes
+
     n, d, b, k, ties = synthetic.CONFIGS[name]
     log(f"[{name}] generating n={n} d={d} b={b} k={k} near_ties={ties}")
     x = synthetic.unit_corpus(n, d, seed=d, device="cuda")
@@ -83,38 +94,74 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
     dev_ms = e0.elapsed_time(e1) / steps
 
-    # Second timed region: the same K calls back to back, with the library
-    # recording HIP events between its launches on the stream it uses.
+    # Second timed region: the same K calls back to back, through the path
+    # Index.search took, with the library recording HIP events between its
+    # launches on the stream it uses.
+    int8 = index._int8_wins(b, k)
     qq = index._prep_queries(q)
+    width = index._x.shape[1]
+
+    def marked(ev):
+        if int8:
+            return eng.q8_topk(qq, index._x, index._xq, k, marks=ev)
+        return eng.fused_topk_marked(qq, index._x, k, ev)
+
     marks = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
     torch.cuda.synchronize()
     for i in range(steps):
-        _, _, plan = eng.fused_topk_marked(qq, index._x, k, marks[i])
+        _, _, plan = marked(marks[i])
     torch.cuda.synchronize()
     per_step = [[m[j].elapsed_time(m[j + 1]) for j in range(4)] for m in marks]
     stage_ms = [statistics.fmean(s[j] for s in per_step) for j in range(4)]
     kern_ms = stage_ms[2]
-    nbytes = kernel_bytes(n, index._x.shape[1], b)
+    dq = q8_row_bytes(width)
+    nbytes = kernel_bytes_q8(n, dq, b) if int8 else kernel_bytes(n, width, b)
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    flops = 2.0 * b * n * d
+    flops = 2.0 * b * n * (dq if int8 else d)
+    mfma_peak = MFMA_INT8_PEAK if int8 else MFMA_FP16_PEAK
+
+    # The other exact path on the same batch, for comparison (not the value).
+    def alt():
+        if int8:
+            return eng.fused_topk(qq, index._x, k)
+        return eng.q8_topk(qq, index._x, index._xq, k) if index._xq is not None else None
+
+    alt_ms = None
+    if alt() is not None:
+        for _ in range(max(2, warmup // 4)):
+            alt()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            alt()
+        torch.cuda.synchronize()
+        alt_ms = (time.perf_counter() - t1) * 1000.0 / steps
     row = {
         "config": name, "n": n, "d": d, "batch": b, "k": k, "near_ties": ties,
         "plan": [int(v) for v in plan.tolist()],
         "ms_per_batch": round(wall_ms, 4), "device_ms_per_batch": round(dev_ms, 4),
         "qps": round(b / (wall_ms / 1000.0), 1),
+        "path": "int8" if int8 else "fused",
         "stage_ms": {"sample_pass": round(stage_ms[0], 4), "threshold_select": round(stage_ms[1], 4),
-                     "scan" if b > 1 else "gemv": round(kern_ms, 4), "final_select": round(stage_ms[3], 4)},
-        "kernel": "scan (MFMA)" if plan.tolist()[0] != 1 else "gemv (v_dot2)",
+                     "scan" if b > 1 else "gemv": round(kern_ms, 4),
+                     "rescore_select" if int8 else "final_select": round(stage_ms[3], 4)},
+        "kernel": (("scan (int8 MFMA)" if int8 else "scan (MFMA)") if plan.tolist()[0] != 1
+                   else ("gemv (int8 v_dot4)" if int8 else "gemv (v_dot2)")),
+        "kernel_bytes": nbytes,
         "kernel_hbm_gbs": round(gbs, 1), "kernel_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "kernel_mfma_frac": round(flops / (kern_ms * 1e-3) / MFMA_FP16_PEAK, 4),
-        "roofline_floor_us": round(max(flops / MFMA_FP16_PEAK, nbytes / (HBM_PEAK_GBS * 1e9)) * 1e6, 2),
+        "kernel_mfma_frac": round(flops / (kern_ms * 1e-3) / mfma_peak, 4),
+        "roofline_floor_us": round(max(flops / mfma_peak, nbytes / (HBM_PEAK_GBS * 1e9)) * 1e6, 2),
+        "other_path": {"path": "fused" if int8 else "int8",
+                       "ms_per_batch": round(alt_ms, 4) if alt_ms is not None else None},
     }
     log(f"[{name}] {json.dumps(row)}")
     return row, (index, q, k, out)
 
 
 # Demangled names of the dominant kernel's dispatches (mode 0 = candidate append).
-DOMINANT = {"scan": re.compile(r"scan_kernel<(?:\d+,\s*){5}0\b"), "gemv": re.compile(r"gemv_kernel<\d+,\s*0>")}
+DOMINANT = {"scan": re.compile(r"scan_kernel<(?:\d+,\s*){5}0\b"), "gemv": re.compile(r"gemv_kernel<\d+,\s*0>"),
+            "scan_q8": re.compile(r"scan_kernel<(?:\d+,\s*){5}4\b"),
+            "gemv_q8": re.compile(r"gemv_kernel<\d+,\s*4>")}
 COPY_KERNEL = re.compile(r"copyBuffer")  # torch copy_ between device tensors = hipMemcpyAsync
 COPY_BYTES = 1 << 30
 
@@ -145,7 +192,17 @@ def pmc_child(name):
     print(f"pmc child {name}: 3 searches, 3 copies of {COPY_BYTES} bytes", flush=True)
 
 
-def measure_traffic(name, batch):
+def dominant_key(name):
+    """Which kernel dominates config `name` on the path Index.search takes."""
+    from cuda_vector_search.index import PAD, int8_auto
+    from cuda_vector_search.synthetic import CONFIGS
+
+    n, d, b, k, _ = CONFIGS[name]
+    key = "gemv" if b == 1 else "scan"
+    return key + "_q8" if int8_auto(n, d + (-d) % PAD, b, k) else key
+
+
+def measure_traffic(name):
     """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc child
     runs; None (with the reason) when rocprofv3 is absent or a run fails."""
     import csv
@@ -155,7 +212,7 @@ def measure_traffic(name, batch):
 
     if shutil.which("rocprofv3") is None:
         return None, "rocprofv3 not on PATH"
-    pat = DOMINANT["gemv" if batch == 1 else "scan"]
+    pat = DOMINANT[dominant_key(name)]
     env = dict(os.environ, TMPDIR="/tmp")
     res = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
@@ -270,9 +327,7 @@ def main():
     # Counter runs first, in child processes, before this process touches the GPU.
     traffic, traffic_detail = (None, "skipped (--no-traffic)")
     if not args.no_traffic:
-        from cuda_vector_search.synthetic import CONFIGS
-
-        traffic, traffic_detail = measure_traffic(names[0], CONFIGS[names[0]][2])
+        traffic, traffic_detail = measure_traffic(names[0])
         log(f"[traffic] {traffic} bytes/launch: {traffic_detail}")
 
     import torch
@@ -318,7 +373,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": round(row["qps"] / REF_T4_QPS_C2, 3) if row["config"] == "C2" else None,
         "vs_baseline_ref": "reference fused kernel on a Tesla T4 (BASELINE.md), not MI355X",
-        "dtype": "fp16 in, fp32 accumulate",
+        "dtype": ("int8 pre-filter (int32 accumulate, rigorous bound) + exact fp16 rescoring (fp32 accumulate)"
+                  if row["path"] == "int8" else "fp16 in, fp32 accumulate"),
         "data": "synthetic: seeded N(0,1) rows, L2-normalised, stored fp16 (cuda_vector_search.synthetic)",
         "config": {"workload": f"{row['config']}: exact top-{k} over {n}x{d} fp16 corpus, batch {b}, "
                                "cosine on unit vectors (ip index)",
@@ -333,7 +389,7 @@ def main():
             "traffic": traffic,
             "traffic_detail": traffic_detail,
             "kernel_ms": kern_ms,
-            "algorithmic_bytes": kernel_bytes(n, d, b),
+            "algorithmic_bytes": row["kernel_bytes"],
             "mfma_frac": row["kernel_mfma_frac"],
         },
         "cpu_baseline": cpu,

@@ -35,7 +35,7 @@ FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-SOURCES = ["cvs_scan.hip", "cvs_select.hip", "cvs_gemv.hip", "cvs_prep.hip", "cvs_capi.hip"]
+SOURCES = ["cvs_scan.hip", "cvs_select.hip", "cvs_gemv.hip", "cvs_prep.hip", "cvs_q8.hip", "cvs_capi.hip"]
 
 # Per-source extra flags.  The scan keeps its MFMA accumulators in VGPRs (the
 # query fragments are pinned in AGPRs explicitly): the epilogue then reads the

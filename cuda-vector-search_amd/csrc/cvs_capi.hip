@@ -163,8 +163,11 @@ struct Plan {
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
 };
 
+// sample_div: the sampling pre-pass scores about 1/sample_div of the tiles (the
+// int8 pre-filter samples more densely: every candidate it keeps costs a
+// random row read, so a tighter threshold pays for itself).
 int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t chunks, int flags,
-              int cus, Plan* p) {
+              int cus, Plan* p, int64_t sample_div = 16) {
   if (k < 1 || k > 256) return fail(CVS_ERR_INVALID, "fused_topk supports 1 <= k <= 256");
   if (k > n) return fail(CVS_ERR_INVALID, "k must not exceed the corpus size");
   if (bq < 0) return fail(CVS_ERR_INVALID, "bq must be 0 (auto) or one of 16, 32, 64, 128, 256");
@@ -188,7 +191,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     P.cap = std::max<int64_t>(128, pow2_at_least(k + 8));
     const int64_t nblocks = ceil_div(n, 64);
     // sampled 64-row blocks, 8 units (row classes mod 8) each
-    const int64_t s = std::min<int64_t>(512, std::max<int64_t>(nblocks / 16, ceil_div(2 * k, 8)));
+    const int64_t s = std::min<int64_t>(8192 / sample_div, std::max<int64_t>(nblocks / sample_div, ceil_div(2 * k, 8)));
     P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
                 (((flags & CVS_FLAG_FORCE_PREPASS) && s <= nblocks) || (s >= 4 && s <= nblocks / 8));
     if (P.prepass) {
@@ -237,7 +240,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     // k * ntiles / s), run by at most one workgroup per CU, each on spt
     // consecutive tiles.
     const int64_t upt = P.cfg.units_per_tile();  // sampling units per tile
-    int64_t s = std::min<int64_t>(1024, std::max<int64_t>(P.ntiles / 16, ceil_div(8 * k, upt)));
+    int64_t s = std::min<int64_t>(16384 / sample_div, std::max<int64_t>(P.ntiles / sample_div, ceil_div(8 * k, upt)));
     s = std::min<int64_t>(s, (flags & CVS_FLAG_FORCE_PREPASS) ? P.ntiles : P.ntiles / 4);
     P.prepass = !(flags & CVS_FLAG_NO_PREPASS) &&
                 (((flags & CVS_FLAG_FORCE_PREPASS) && s >= 1) || (s >= 4 && s * upt >= 2 * k));
@@ -680,6 +683,394 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
   hipError_t e = launch_prep(a, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "row preparation launch");
   return CVS_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// int8 pre-filter (no counterpart in the reference): an int8 companion of the
+// corpus is scanned instead of the fp16 rows, rows whose score upper bound
+// reaches the sampled threshold are kept, and their exact fp16 scores are
+// recomputed by the select kernel.  Results equal cvs_fused_topk's.
+
+namespace {
+
+constexpr int64_t kQ8SampleDiv = 8;
+
+// int8 row bytes for a row of d fp16 elements: one of the widths the int8
+// scan is instantiated for.
+int64_t q8_row_bytes(int64_t d) { return d <= 384 ? 384 : d <= 768 ? 768 : 1536; }
+
+struct Q8Layout {
+  int64_t dq = 0, rows = 0, nblk = 0, off_meta = 0, off_xmax = 0, bytes = 0;
+};
+
+Q8Layout q8_layout(int64_t n, int64_t d) {
+  Q8Layout L;
+  L.dq = q8_row_bytes(d);
+  L.nblk = ceil_div(n, 64);
+  L.rows = L.nblk * 64;
+  L.off_meta = align_up(L.rows * L.dq, 256);
+  L.off_xmax = L.off_meta + L.nblk * 16;
+  L.bytes = L.off_xmax + 16;
+  return L;
+}
+
+struct Q8Plan {
+  Plan sample;  // fp16 plan: only its sampling pre-pass (scan or GEMV) is used
+  bool gemv = false;  // batch 1: int8 GEMV instead of the int8 scan
+  int64_t gemv_grid = 0, rows_per_wave = 0;
+  ScanCfg cfg{};
+  int64_t dq = 0, bq = 0, groups = 1, chunks = 1, ntiles = 0, tpc = 0, nlists = 0, cap = 0;
+  int xcd_pair = 0;
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_qq = 0, off_qm = 0, ws_bytes = 0;
+};
+
+int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus, Q8Plan* out) {
+  Q8Plan P;
+  int rc = make_plan(nq, n, d, k, 0, 0, flags, cus, &P.sample, kQ8SampleDiv);
+  if (rc != CVS_OK) return rc;
+  P.dq = q8_row_bytes(d);
+  const int ks = (int)(P.dq / 32);
+  P.gemv = (nq == 1 && !(flags & CVS_FLAG_NO_GEMV));
+  if (P.gemv) {  // per-wave row ranges as the fp16 GEMV path
+    int64_t waves = (int64_t)cus * 16;
+    waves = std::max<int64_t>(1, std::min<int64_t>({waves, kSelectMaxLists, ceil_div(n, 16)}));
+    P.gemv_grid = ceil_div(waves, 4);
+    waves = P.gemv_grid * 4;
+    P.rows_per_wave = align_up(ceil_div(n, waves), 16);
+    P.bq = 1;
+    P.chunks = waves;
+    P.nlists = waves;
+    P.ntiles = waves;
+    P.tpc = 1;
+    P.cfg = {32, 1, 1, 1, ks};  // unused (tile/row mapping below uses rows_per_wave)
+  } else if (nq <= 32 || (nq <= 64 && ks == 48)) {
+    P.cfg = {32, 1, 1, 1, ks};
+  } else if (nq <= 64) {
+    P.cfg = {32, 1, 2, 1, ks};
+  } else if (nq <= 128 || ks == 48) {
+    P.cfg = {32, 4, 1, 2, ks};
+  } else {
+    P.cfg = {32, 8, 1, 2, ks};
+  }
+  if (!scan_cfg_available(P.cfg, kAppendQ8)) return fail(CVS_ERR_INVALID, "internal: no int8 scan for width %lld", (long long)d);
+  if (!P.gemv) {
+  P.bq = P.cfg.bq();
+  P.groups = ceil_div(std::max<int64_t>(nq, 1), P.bq);
+  P.ntiles = ceil_div(n, P.cfg.tile_rows());
+  const int64_t rs = P.cfg.rs();
+  const int64_t max_chunks = std::min<int64_t>({P.ntiles, 65535, kSelectMaxLists / rs});
+  int64_t c = std::max<int64_t>(1, ceil_div(cus, P.groups));
+  c = std::min<int64_t>(c, std::max<int64_t>(1, P.ntiles / 2));
+  c = std::min<int64_t>(c, max_chunks);
+  if (P.groups > 1 && c >= 8) {
+    c = std::min<int64_t>(align_up(c, 8), (max_chunks / 8) * 8);
+    P.tpc = ceil_div(P.ntiles, c);
+  } else {
+    P.tpc = ceil_div(P.ntiles, c);
+    c = ceil_div(P.ntiles, P.tpc);
+  }
+  P.chunks = c;
+  P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
+  P.nlists = c * rs;
+  }
+  P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
+  if (P.groups * P.chunks > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
+  const int64_t nqq = std::max<int64_t>(nq, 1);
+  const int64_t lists = nqq * P.nlists;
+  int64_t off = 0;
+  P.off_lv = off;
+  off = align_up(off + lists * P.cap * 4, 256);
+  P.off_li = off;
+  off = align_up(off + lists * P.cap * 4, 256);
+  P.off_cnt = off;
+  off = align_up(off + lists * 4, 256);
+  P.off_tau = off;
+  off = align_up(off + nqq * 4, 256);
+  P.off_umax = off;
+  if (P.sample.prepass) off = align_up(off + nqq * P.sample.units * 4, 256);
+  P.off_qq = off;
+  off = align_up(off + nqq * P.dq, 256);
+  P.off_qm = off;
+  off = align_up(off + nqq * 16, 256);
+  P.ws_bytes = off;
+  *out = P;
+  return CVS_OK;
+}
+
+int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64_t nq, int64_t n, int64_t d,
+           int64_t k, int flags, void* workspace, int64_t workspace_bytes, float* out_v, void* out_i,
+           int64_t* plan_out, int device, void* stream, hipEvent_t* marks) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  rc = check_inputs(q, x, nq, n, d);
+  if (rc != CVS_OK) return rc;
+  Q8Plan P;
+  rc = make_q8_plan(nq, n, d, k, flags, di.cus, &P);
+  if (rc != CVS_OK) return rc;
+  if (plan_out) {
+    plan_out[0] = P.bq;
+    plan_out[1] = P.chunks;
+  }
+  if (nq == 0) return CVS_OK;
+  const Q8Layout L = q8_layout(n, d);
+  if (xq == nullptr || reinterpret_cast<uintptr_t>(xq) % 256 != 0)
+    return fail(CVS_ERR_INVALID, "int8 corpus must be 256-byte aligned");
+  if (xq_bytes < L.bytes)
+    return fail(CVS_ERR_INVALID, "int8 corpus too small: need %lld bytes, got %lld", (long long)L.bytes, (long long)xq_bytes);
+  if (out_v == nullptr || out_i == nullptr) return fail(CVS_ERR_INVALID, "output pointers must not be null");
+  if (workspace == nullptr || workspace_bytes < P.ws_bytes)
+    return fail(CVS_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)P.ws_bytes,
+                (long long)workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(CVS_ERR_INVALID, "workspace must be 256-byte aligned");
+
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto mark = [&](int i) {
+    if (marks) (void)hipEventRecord(marks[i], s);
+  };
+  mark(0);
+  char* ws = static_cast<char*>(workspace);
+  float* lv = reinterpret_cast<float*>(ws + P.off_lv);
+  int* li = reinterpret_cast<int*>(ws + P.off_li);
+  int* cnt = reinterpret_cast<int*>(ws + P.off_cnt);
+  float* tau = reinterpret_cast<float*>(ws + P.off_tau);
+  float* umax = reinterpret_cast<float*>(ws + P.off_umax);
+  signed char* qq = reinterpret_cast<signed char*>(ws + P.off_qq);
+  float4* qm = reinterpret_cast<float4*>(ws + P.off_qm);
+  const _Float16* qh = static_cast<const _Float16*>(q);
+  const _Float16* xh = static_cast<const _Float16*>(x);
+  const Plan& S = P.sample;
+  hipError_t e;
+
+  if (!S.prepass) {  // otherwise the threshold select quantises the queries on the way
+    Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm};
+    e = launch_q8_queries(qa, s);
+    if (e != hipSuccess) return hip_fail(e, "query quantisation launch");
+  }
+  if (S.prepass) {  // exact fp16 sampling pre-pass and threshold, as in cvs_fused_topk
+    if (S.gemv) {
+      GemvArgs pg{};
+      pg.q = qh;
+      pg.x = xh;
+      pg.n = n;
+      pg.d = (int)d;
+      pg.rows_per_wave = S.rows_per_wave;
+      pg.k = (int)k;
+      pg.cap = (int)S.cap;
+      pg.mode = kMax;
+      pg.umax = umax;
+      pg.nsample = (int)S.nsample;
+      pg.upb = S.upb;
+      pg.units = (int)S.units;
+      e = launch_gemv(ks_bucket(d) * 32, pg, (int)ceil_div(S.nsample, 4), s);
+    } else {
+      ScanArgs pa{};
+      pa.q = qh;
+      pa.x = xh;
+      pa.n = n;
+      pa.nq = (int)nq;
+      pa.d = (int)d;
+      pa.groups = (int)S.groups;
+      pa.nchunks = (int)S.chunks;
+      pa.ntiles = S.ntiles;
+      pa.tpc = S.tpc;
+      pa.k = (int)k;
+      pa.cap = (int)S.cap;
+      pa.umax = umax;
+      pa.nsample = (int)S.nsample;
+      pa.spt = (int)S.spt;
+      pa.agg = S.agg;
+      pa.units = (int)S.units;
+      e = launch_scan(S.cfg, kMax, pa, (int)(S.groups * S.nsample), s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "sample pass launch");
+    SelectArgs sa{};
+    sa.lv = umax;
+    sa.nlists = 1;
+    sa.cap = (int)S.units;
+    sa.k = (int)k;
+    sa.tau = tau;
+    sa.q = qh;
+    sa.d = (int)d;
+    sa.qq_out = qq;
+    sa.qmeta_out = qm;
+    sa.dq = (int)P.dq;
+    mark(1);
+    e = launch_select(1, sa, (int)nq, s);
+    if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+    mark(2);
+  } else {
+    mark(1);
+    mark(2);
+  }
+  const float4* bmeta = reinterpret_cast<const float4*>(static_cast<const char*>(xq) + L.off_meta);
+  const float gamma = (float)(3 * d + 8) / 16777216.0f;
+  if (P.gemv) {
+    GemvArgs g{};
+    g.q = reinterpret_cast<const _Float16*>(qq);
+    g.x = static_cast<const _Float16*>(xq);
+    g.n = n;
+    g.d = (int)P.dq;  // int8 row bytes
+    g.rows_per_wave = P.rows_per_wave;
+    g.tau = S.prepass ? tau : nullptr;
+    g.lv = lv;
+    g.li = li;
+    g.lcount = cnt;
+    g.nlists = (int)P.nlists;
+    g.cap = (int)P.cap;
+    g.k = (int)k;
+    g.mode = kAppendQ8;
+    g.qmeta = qm;
+    g.bmeta = bmeta;
+    g.gamma = gamma;
+    e = launch_gemv(1536, g, (int)P.gemv_grid, s);
+    if (e != hipSuccess) return hip_fail(e, "int8 gemv launch");
+  } else {
+  ScanArgs a{};
+  a.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
+  a.x = static_cast<const _Float16*>(xq);
+  a.n = n;
+  a.nq = (int)nq;
+  a.d = (int)(P.dq / 2);
+  a.groups = (int)P.groups;
+  a.nchunks = (int)P.chunks;
+  a.ntiles = P.ntiles;
+  a.tpc = P.tpc;
+  a.xcd_pair = P.xcd_pair;
+  a.tau = S.prepass ? tau : nullptr;
+  a.lv = lv;
+  a.li = li;
+  a.lcount = cnt;
+  a.nlists = (int)P.nlists;
+  a.cap = (int)P.cap;
+  a.k = (int)k;
+  a.qmeta = qm;
+  a.bmeta = bmeta;
+  a.gamma = gamma;
+  e = launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
+  if (e != hipSuccess) return hip_fail(e, "int8 scan launch");
+  }
+  mark(3);
+  SelectArgs fa{};
+  fa.lv = lv;
+  fa.li = li;
+  fa.lcount = cnt;
+  fa.nlists = (int)P.nlists;
+  fa.cap = (int)P.cap;
+  fa.k = (int)k;
+  fa.out_v = out_v;
+  fa.out_i = out_i;
+  fa.ids64 = (flags & CVS_FLAG_IDS_INT64) ? 1 : 0;
+  fa.q = qh;
+  fa.x = xh;
+  fa.n = n;
+  fa.d = (int)d;
+  fa.ntiles = P.ntiles;
+  fa.tpc = P.tpc;
+  if (P.gemv) {  // list L = rows [L * rows_per_wave, (L + 1) * rows_per_wave)
+    fa.tile_rows = (int)P.rows_per_wave;
+    fa.wave_rows = (int)P.rows_per_wave;
+    fa.rsplits = 1;
+  } else {
+    fa.tile_rows = P.cfg.tile_rows();
+    fa.wave_rows = P.cfg.wave_rows();
+    fa.rsplits = P.cfg.rs();
+  }
+  // rescoring: about 4 workgroups per CU over (query, group of lists)
+  fa.tau_in = S.prepass ? tau : nullptr;
+  fa.qmeta = qm;
+  fa.xmax = reinterpret_cast<const float*>(static_cast<const char*>(xq) + L.off_xmax);
+  fa.gamma = (float)d / 16777216.0f;
+  fa.lpb = 256;
+  while (fa.lpb > 8 && nq * ceil_div(P.nlists, fa.lpb) < 4 * (int64_t)di.cus) fa.lpb /= 2;
+  e = launch_rescore(fa, (int)nq, s);
+  if (e != hipSuccess) return hip_fail(e, "rescore launch");
+  e = launch_select(2, fa, (int)nq, s);
+  if (e != hipSuccess) return hip_fail(e, "rescore select launch");
+  mark(4);
+  return CVS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cvs_q8_corpus_bytes(int64_t n, int64_t d, int64_t* bytes) {
+  if (bytes == nullptr) return fail(CVS_ERR_INVALID, "bytes must not be null");
+  if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
+  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (n < 1 || n >= INT_MAX) return fail(CVS_ERR_INVALID, "corpus must have between 1 and 2^31-1 rows");
+  *bytes = q8_layout(n, d).bytes;
+  return CVS_OK;
+}
+
+int cvs_q8_build(const void* x, int64_t n, int64_t d, void* xq, int64_t xq_bytes, int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  int64_t need = 0;
+  rc = cvs_q8_corpus_bytes(n, d, &need);
+  if (rc != CVS_OK) return rc;
+  if (x == nullptr || reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(CVS_ERR_INVALID, "corpus must be 16-byte aligned");
+  if (xq == nullptr || reinterpret_cast<uintptr_t>(xq) % 256 != 0)
+    return fail(CVS_ERR_INVALID, "int8 corpus must be 256-byte aligned");
+  if (xq_bytes < need)
+    return fail(CVS_ERR_INVALID, "int8 corpus too small: need %lld bytes, got %lld", (long long)need, (long long)xq_bytes);
+  const Q8Layout L = q8_layout(n, d);
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  Q8BuildArgs a{static_cast<const _Float16*>(x), n, (int)d, (int)L.dq, static_cast<signed char*>(xq),
+                reinterpret_cast<float4*>(static_cast<char*>(xq) + L.off_meta),
+                reinterpret_cast<unsigned*>(static_cast<char*>(xq) + L.off_xmax)};
+  hipError_t e = hipMemsetAsync(a.xmax, 0, 16, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+  e = launch_q8_build(a, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "int8 corpus build launch");
+  return CVS_OK;
+}
+
+int cvs_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int device, int64_t* plan_out,
+                int64_t* workspace_bytes) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
+  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  Q8Plan P;
+  rc = make_q8_plan(nq, n, d, k, flags, di.cus, &P);
+  if (rc != CVS_OK) return rc;
+  if (plan_out) {
+    plan_out[0] = P.bq;
+    plan_out[1] = P.chunks;
+  }
+  if (workspace_bytes) *workspace_bytes = P.ws_bytes;
+  return CVS_OK;
+}
+
+int cvs_q8_topk(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64_t nq, int64_t n, int64_t d,
+                int64_t k, int flags, void* workspace, int64_t workspace_bytes, float* out_v, void* out_i,
+                int64_t* plan_out, int device, void* stream) {
+  return run_q8(q, x, xq, xq_bytes, nq, n, d, k, flags, workspace, workspace_bytes, out_v, out_i, plan_out, device,
+                stream, nullptr);
+}
+
+int cvs_q8_topk_marked(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64_t nq, int64_t n,
+                       int64_t d, int64_t k, int flags, void* workspace, int64_t workspace_bytes, float* out_v,
+                       void* out_i, int64_t* plan_out, int device, void* stream, void* const* marks) {
+  if (marks == nullptr) return fail(CVS_ERR_INVALID, "marks must not be null");
+  hipEvent_t ev[5];
+  for (int i = 0; i < 5; ++i) {
+    if (marks[i] == nullptr) return fail(CVS_ERR_INVALID, "marks[%d] is null", i);
+    ev[i] = reinterpret_cast<hipEvent_t>(marks[i]);
+  }
+  return run_q8(q, x, xq, xq_bytes, nq, n, d, k, flags, workspace, workspace_bytes, out_v, out_i, plan_out, device,
+                stream, nq > 0 ? ev : nullptr);
 }
 
 }  // extern "C"

@@ -9,6 +9,11 @@
 // stays in VGPRs.  Rows are split into contiguous per-wave ranges (long
 // sequential streams per wave).  Scores are filtered against the threshold and
 // survivors appended to the wave's candidate list, exactly as in the scan path.
+//
+// kAppendQ8 is the same kernel over the int8 companion of the corpus
+// (v_dot4_i32_i8, exact int32 sums, 128-byte pieces of 128 int8): rows whose
+// score upper bound reaches the threshold are appended, a full list is marked
+// overflowed instead of compacted, and the select recomputes exact scores.
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 
@@ -17,6 +22,18 @@ namespace cvs {
 namespace {
 
 constexpr int kUnr = 2;  // 8-row groups per wave per iteration
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 16 int8 x 16 int8, exact.
+__device__ __forceinline__ int dot16_i8(half8 a, half8 b, int acc) {
+  const i32x4 x = __builtin_bit_cast(i32x4, a), y = __builtin_bit_cast(i32x4, b);
+  acc = __builtin_amdgcn_sdot4(x[0], y[0], acc, false);
+  acc = __builtin_amdgcn_sdot4(x[1], y[1], acc, false);
+  acc = __builtin_amdgcn_sdot4(x[2], y[2], acc, false);
+  acc = __builtin_amdgcn_sdot4(x[3], y[3], acc, false);
+  return acc;
+}
 
 __device__ __forceinline__ float dot8(half8 a, half8 b, float acc) {
   acc = __builtin_amdgcn_fdot2(half2v{a[0], a[1]}, half2v{b[0], b[1]}, acc, false);
@@ -29,21 +46,28 @@ __device__ __forceinline__ float dot8(half8 a, half8 b, float acc) {
 // PMAX = max 128-byte pieces per row handled by one lane (d <= 64*PMAX).
 template <int PMAX, int MODE>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
+  constexpr bool Q8 = (MODE == kAppendQ8);
+  constexpr bool APP = (MODE == kAppend || Q8);
   __shared__ uint64_t sortbuf[MODE == kAppend ? 4 * kMaxCap : 1];
   const int lane = lane_id();
   const int w = threadIdx.x >> 6;
   const int sub = lane & 7;     // 16-byte slot within a 128-byte piece
   const int rg = lane >> 3;     // row within an 8-row group
   const int gw = blockIdx.x * 4 + w;
-  const int d = a.d;
-  const int np = d >> 6;
+  const int d = a.d;            // row elements (fp16) or bytes (int8)
+  const int np = Q8 ? d >> 7 : d >> 6;  // 128-byte pieces per row
+  const int64_t rb = Q8 ? d : 2 * (int64_t)d;  // row bytes
   const int64_t n = a.n;
+  const unsigned char* xb = reinterpret_cast<const unsigned char*>(a.x);
+  const unsigned char* qb = reinterpret_cast<const unsigned char*>(a.q);
 
   // Unconditional loads (a piece past d re-reads the last one and is never
   // used): a per-load branch would put each behind a wait for the previous one.
   half8 qv[PMAX];
 #pragma unroll
-  for (int p = 0; p < PMAX; ++p) qv[p] = *(const half8*)(a.q + min(p, np - 1) * 64 + sub * 8);
+  for (int p = 0; p < PMAX; ++p) qv[p] = *(const half8*)(qb + min(p, np - 1) * 128 + sub * 16);
+  float4 qm = float4{0.f, 0.f, 0.f, 0.f};
+  if (Q8) qm = a.qmeta[0];
 
   int64_t r_begin, r_end;
   if (MODE == kMax) {
@@ -57,12 +81,12 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
     r_end = r_begin + a.rows_per_wave < n ? r_begin + a.rows_per_wave : n;
   }
 
-  float thr = (MODE == kAppend && a.tau) ? a.tau[0] : -__builtin_inff();
+  float thr = (APP && a.tau) ? a.tau[0] : -__builtin_inff();
   float umax = -__builtin_inff();  // kMax: best score of this lane group's rows
   int count = 0;
   float* lv = nullptr;
   int* li = nullptr;
-  if (MODE == kAppend) {
+  if (APP) {
     lv = a.lv + (int64_t)gw * a.cap;
     li = a.li + (int64_t)gw * a.cap;
   }
@@ -73,20 +97,43 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
     for (int u = 0; u < kUnr; ++u) {
       int64_t row = r0 + u * 8 + rg;
       if (row >= n) row = n - 1;
-      const _Float16* src = a.x + row * d + sub * 8;
+      const unsigned char* src = xb + row * rb + sub * 16;
 #pragma unroll
       for (int p = 0; p < PMAX; ++p)
-        if (p < np) xv[u][p] = __builtin_nontemporal_load((const half8*)(src + p * 64));
+        if (p < np) xv[u][p] = __builtin_nontemporal_load((const half8*)(src + p * 128));
+    }
+    // kAppendQ8: the 16 rows of this iteration lie in one 64-row block
+    // (per-wave ranges start at multiples of 16); its meta comes through the
+    // scalar cache.
+    float cq = 0.f, slack = 0.f;
+    if (Q8) {
+      typedef const __attribute__((address_space(4))) float* cfloat_p;
+      const int blk = __builtin_amdgcn_readfirstlane((int)(min(r0, n - 1) >> 6));
+      const cfloat_p m = (cfloat_p)a.bmeta + 4 * (int64_t)blk;
+      const float bs = m[0], bf = m[1], bx = m[2];
+      cq = qm.x * bs;
+      slack = (fmaf(qm.y, bf, qm.z * bx) + a.gamma * (qm.y + qm.z) * (bf + bx)) * (1.0f + 1.0f / 1048576.0f);
     }
 #pragma unroll
     for (int u = 0; u < kUnr; ++u) {
       float acc = 0.f;
+      if (Q8) {
+        int ia = 0;
 #pragma unroll
-      for (int p = 0; p < PMAX; ++p)
-        if (p < np) acc = dot8(xv[u][p], qv[p], acc);
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 4);
+        for (int p = 0; p < PMAX; ++p)
+          if (p < np) ia = dot16_i8(xv[u][p], qv[p], ia);
+        ia += __shfl_xor(ia, 1);
+        ia += __shfl_xor(ia, 2);
+        ia += __shfl_xor(ia, 4);
+        acc = fmaf((float)ia, cq, slack);  // upper bound of the exact score
+      } else {
+#pragma unroll
+        for (int p = 0; p < PMAX; ++p)
+          if (p < np) acc = dot8(xv[u][p], qv[p], acc);
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        acc += __shfl_xor(acc, 4);
+      }
       const int64_t row = r0 + u * 8 + rg;
       const bool valid = row < r_end;
       if (MODE == kMax) {
@@ -94,7 +141,15 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       } else {
         bool pass = valid && sub == 0 && acc >= thr;
         uint64_t mask = __ballot(pass);
-        if (mask) {
+        if (mask && Q8) {  // no compaction: a full list overflows (count > cap)
+          const int nnew = __popcll(mask);
+          if (pass && count + nnew <= a.cap) {
+            const int pos = count + lanes_below(mask);
+            lv[pos] = acc;
+            li[pos] = (int)row;
+          }
+          count = (count + nnew <= a.cap) ? count + nnew : a.cap + 1;
+        } else if (mask) {
           int nnew = __popcll(mask);
           if (count + nnew > a.cap) {
             thr = fmaxf(thr, wave_compact(lv, li, count, a.k, sortbuf + w * kMaxCap));
@@ -126,7 +181,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       a.umax[(int64_t)gw * 8 + rg] = umax;
     }
   }
-  if (MODE == kAppend && lane == 0) a.lcount[gw] = count;
+  if (APP && lane == 0) a.lcount[gw] = count;
 }
 
 template <int PMAX>
@@ -140,9 +195,22 @@ hipError_t launch_p(const GemvArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int PMAX>
+hipError_t launch_q8(const GemvArgs& a, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_kernel<PMAX, kAppendQ8>), dim3(grid), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s) {
+  if (a.mode == kAppendQ8) {  // d = int8 row bytes
+    if (a.qmeta == nullptr || a.bmeta == nullptr || a.rows_per_wave % 16 != 0) return hipErrorInvalidValue;
+    if (a.d == 384) return launch_q8<3>(a, grid, s);
+    if (a.d == 768) return launch_q8<6>(a, grid, s);
+    if (a.d == 1536) return launch_q8<12>(a, grid, s);
+    return hipErrorInvalidValue;
+  }
   if (a.d > dmax) return hipErrorInvalidValue;
   if (dmax <= 384) return launch_p<6>(a, grid, s);
   if (dmax <= 768) return launch_p<12>(a, grid, s);

@@ -12,6 +12,8 @@ enum ScanMode : int {
   kMax = 1,       // sample pass: per-(query, unit) maxima over disjoint row sets
   kStoreF32 = 2,  // write the full score matrix (fp32)
   kStoreF16 = 3,  // write the full score matrix (fp16)
+  kAppendQ8 = 4,  // int8 pre-filter: int8 rows x int8 queries, append rows whose score
+                  // upper bound reaches the threshold (no compaction; full lists overflow)
 };
 
 // One tile of corpus rows is scored against a group of queries by one
@@ -45,6 +47,10 @@ struct ScanArgs {
   int units;          // units per query = nsample * (agg ? 1 : spt) * units_per_tile
   // kStore*
   void* out;          // [nq, n]
+  // kAppendQ8 (q, x are int8 rows viewed as 2-byte units: d = row bytes / 2)
+  const float4* qmeta;  // [nq] (s_q, |q^|_2 up, |e_q|_2 up, 0): query scale and residual norms
+  const float4* bmeta;  // [ceil(n/64)] (s_b, max |f_r|_2 up, max |x_r|_2 up, 0) per 64-row block
+  float gamma;          // relative slack for fp32 rounding of the scores: (3d + 8) * 2^-24
 };
 
 // Batch-1 GEMV: one query, rows split across waves, 8 lanes per row.
@@ -65,7 +71,12 @@ struct GemvArgs {
   int nsample;        // kMax: sampled 64-row blocks (one per wave)
   int upb;            // kMax: units per block, 8 (rows mod 8) or 1 (the block)
   int units;
-  int mode;           // kAppend or kMax
+  int mode;           // kAppend, kMax or kAppendQ8
+  // kAppendQ8: q and x are int8 rows of d bytes (d = 384, 768 or 1536); the
+  // filter uses the score upper bound as the scan's kAppendQ8 does
+  const float4* qmeta;  // [1]
+  const float4* bmeta;  // [ceil(n/64)]
+  float gamma;
 };
 
 // Row top-k, first stage: one workgroup per (row, chunk of `len` columns).
@@ -104,6 +115,48 @@ struct SelectArgs {
   void* out_i;         // [nq, k] int32, or int64 when ids64 (final mode)
   int ids64;
   float* tau;          // [nq]    (threshold mode: score of the k-th best)
+  // rescore mode: candidates are row ids only; their exact fp16 scores are
+  // recomputed here.  A list whose count exceeds cap overflowed in the scan and
+  // stands for every row of its range, all of which are rescored.
+  const _Float16* q;   // [nq, d]
+  const _Float16* x;   // [n, d]
+  int64_t n;
+  int d;
+  int64_t ntiles, tpc; // the scan's tiles and tiles per chunk
+  int tile_rows, wave_rows, rsplits;  // list L = chunk * rsplits + r
+  int lpb;             // rescore kernel: lists per workgroup
+  // rescore kernel: candidates whose exact score is below the sampled
+  // threshold by more than the fp32 rounding slack are dropped
+  const float* tau_in;    // [nq] sampled thresholds, or null (keep everything)
+  const float4* qmeta;    // [nq] (s_q, |q^|, |e|, 0)
+  const float* xmax;      // max |x_r|_2 over the corpus (rounded up)
+  float gamma;            // d * 2^-24 (one rounding per accumulated term)
+  // threshold mode, int8 pre-filter: also quantise query row q (q, d above)
+  // into qq_out[q * dq ..] and qmeta_out[q] (when qq_out is not null)
+  signed char* qq_out;
+  float4* qmeta_out;
+  int dq;
+};
+
+// int8 companion of an fp16 corpus: rows quantised per 64-row block.
+struct Q8BuildArgs {
+  const _Float16* x;   // [n, d]
+  int64_t n;
+  int d;
+  int dq;              // int8 row bytes (>= d, multiple of 128); columns d..dq are zero
+  signed char* xq;     // [ceil(n/64)*64, dq]
+  float4* bmeta;       // [ceil(n/64)]
+  unsigned* xmax;      // max over blocks of max|x_r|_2 (float bits; zeroed before the launch)
+};
+
+// int8 queries: per-query scale and residual norms.
+struct Q8QueryArgs {
+  const _Float16* q;   // [nq, d]
+  int64_t nq;
+  int d;
+  int dq;
+  signed char* qq;     // [nq, dq]
+  float4* qmeta;       // [nq]
 };
 
 // Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,
@@ -121,9 +174,12 @@ struct ScanCfg {
 // Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
 hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
-hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s);
+hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);  // 0 final, 1 threshold, 2 rescore
 hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
 hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s);
+hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s);
+hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);
+hipError_t launch_q8_queries(const Q8QueryArgs& a, hipStream_t s);
 
 bool scan_cfg_available(const ScanCfg& cfg, int mode);
 

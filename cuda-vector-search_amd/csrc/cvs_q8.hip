@@ -1,0 +1,138 @@
+// int8 companion of the fp16 corpus and of each query batch, for the int8
+// pre-filter of the exact search (no counterpart in the reference, whose only
+// corpus format is the fp16 matrix of cuda_vector_search/index.py:56-78).
+//
+// Rows are quantised symmetrically: a 64-row block of the corpus shares one
+// scale s_b = max|x| / 127 over the block, a query row has its own s_q, and
+// x~ = rint(x * (127 / max)) in [-127, 127].  The scan then computes
+// A = s_q * s_b * sum(q~ x~) with int8 MFMAs (exact int32 sums), and
+//
+//     |q.x - A| <= |q^|_2 |f|_2 + |e|_2 |x|_2,   q^ = s_q q~, e = q - q^,
+//                                                 f = x - s_b x~
+//
+// (Cauchy-Schwarz on the two residuals), so the exact score of every row lies
+// within that slack of A.  The kernels here store, per block, s_b and upper
+// bounds of max |f_r|_2 and max |x_r|_2 over its rows, and per query s_q,
+// |q^|_2 and |e|_2 (norms rounded up to cover fp32 accumulation).
+#include "cvs_common.h"
+#include "cvs_kernels.h"
+#include "cvs_q8_row.h"
+
+namespace cvs {
+
+namespace {
+
+constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;  // > 1 + d * 2^-24 for d <= 8192, plus sqrt's ulp
+
+
+// One workgroup per 64-row block; thread t takes row t/4 and the 8-element
+// pieces p = t%4, t%4 + 4, ... of it (4 consecutive lanes read 64 contiguous
+// bytes).  Pass 1: block max |x|; pass 2 (re-reading the rows, now in cache):
+// quantise, write the int8 row and its zero padding, and reduce the row's
+// residual and value norms.
+__global__ __launch_bounds__(kBlock) void q8_build_kernel(Q8BuildArgs a) {
+  __shared__ float red[kBlock / kWave];
+  __shared__ float fmax_s[kBlock / kWave], xmax_s[kBlock / kWave];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int64_t blk = blockIdx.x;
+  const int64_t row = blk * 64 + (tid >> 2);
+  const int part = tid & 3;
+  const bool live = row < a.n;
+  const int pieces = a.d / 8;  // 8-element pieces per row
+  const half8* src = reinterpret_cast<const half8*>(a.x + (live ? row : 0) * (int64_t)a.d);
+
+  float m = 0.f;
+  if (live) {
+    for (int p = part; p < pieces; p += 4) {
+      const half8 v = src[p];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf((float)v[j]));
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) red[w] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = M / 127.f;
+  const float inv = M > 0.f ? 127.f / M : 0.f;
+
+  signed char* dst = a.xq + row * (int64_t)a.dq;
+  float ff = 0.f, xx = 0.f;
+  for (int p = part; p < pieces; p += 4) {
+    half8 v = {};
+    if (live) v = src[p];
+    int2 packed;
+    unsigned lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float xv = (float)v[j];
+      const signed char c = q8_quant(xv, inv);
+      const float f = fmaf(-s, (float)c, xv);
+      ff = fmaf(f, f, ff);
+      xx = fmaf(xv, xv, xx);
+      if (j < 4) lo |= (unsigned)(unsigned char)c << (8 * j);
+      else hi |= (unsigned)(unsigned char)c << (8 * (j - 4));
+    }
+    packed.x = (int)lo;
+    packed.y = (int)hi;
+    *reinterpret_cast<int2*>(dst + 8 * p) = packed;
+  }
+  for (int c = a.d + 8 * part; c < a.dq; c += 32) *reinterpret_cast<int2*>(dst + c) = int2{0, 0};
+  // row norms: the row's 4 threads are consecutive lanes
+  ff += __shfl_xor(ff, 1);
+  ff += __shfl_xor(ff, 2);
+  xx += __shfl_xor(xx, 1);
+  xx += __shfl_xor(xx, 2);
+  float fn = sqrtf(ff) * kNormUp, xn = sqrtf(xx) * kNormUp;
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    fn = fmaxf(fn, __shfl_xor(fn, off));
+    xn = fmaxf(xn, __shfl_xor(xn, off));
+  }
+  if (lane == 0) {
+    fmax_s[w] = fn;
+    xmax_s[w] = xn;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float4 meta;
+    meta.x = s;
+    meta.y = fmaxf(fmaxf(fmax_s[0], fmax_s[1]), fmaxf(fmax_s[2], fmax_s[3]));
+    meta.z = fmaxf(fmaxf(xmax_s[0], xmax_s[1]), fmaxf(xmax_s[2], xmax_s[3]));
+    meta.w = 0.f;
+    a.bmeta[blk] = meta;
+    atomicMax(a.xmax, __float_as_uint(meta.z));  // non-negative floats order as their bits
+  }
+}
+
+// One wave per query row.
+__global__ __launch_bounds__(kBlock) void q8_query_kernel(Q8QueryArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
+  if (r >= a.nq) return;  // whole wave
+  q8_query_row(a.q + r * a.d, a.d, a.dq, a.qq + r * a.dq, a.qmeta + r, threadIdx.x & 63);
+}
+
+}  // namespace
+
+hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
+  if (a.d < 8 || a.d % 8 != 0 || a.dq < a.d || a.dq % 128 != 0) return hipErrorInvalidValue;
+  const int64_t blocks = (a.n + 63) / 64;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(q8_build_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_queries(const Q8QueryArgs& a, hipStream_t s) {
+  if (a.d < 1 || a.d > kQ8RowPer * kWave || a.dq < a.d || a.dq > kQ8RowPer * kWave || a.dq % 128 != 0)
+    return hipErrorInvalidValue;
+  const int64_t per = kBlock / kWave;
+  const int64_t grid = (a.nq + per - 1) / per;
+  if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(q8_query_kernel, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace cvs

@@ -1,0 +1,61 @@
+// Per-row int8 quantisation of a query, one wave per row (shared by the query
+// quantisation kernel and the threshold select, which does it on the way).
+// s = max|q| / 127, q~ = clip(rint(q * (127 / max)), -127, 127); meta = (s,
+// s |q~|_2, |q - s q~|_2, 0) with the two norms rounded up (fp32 sums of at
+// most 1536 terms: relative error < 2^-13, covered by the 2^-11 factor).
+#pragma once
+
+#include "cvs_common.h"
+
+namespace cvs {
+
+constexpr int kQ8RowPer = 24;  // d <= 1536 = 24 elements per lane
+
+__device__ __forceinline__ signed char q8_quant(float v, float inv) {
+  const float r = rintf(v * inv);
+  return (signed char)fminf(127.f, fmaxf(-127.f, r));
+}
+
+// Whole wave; `lane` = lane id.  dst holds dq >= d bytes (zero past d).
+__device__ __forceinline__ void q8_query_row(const _Float16* src, int d, int dq, signed char* dst, float4* meta,
+                                             int lane) {
+  constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;
+  float v[kQ8RowPer];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < kQ8RowPer; ++i) {
+    const int c = i * kWave + lane;
+    v[i] = c < d ? (float)src[c] : 0.f;
+    m = fmaxf(m, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const float s = m / 127.f;
+  const float inv = m > 0.f ? 127.f / m : 0.f;
+  int sq = 0;  // sum of q~^2, exact (< 1536 * 127^2)
+  float ee = 0.f;
+#pragma unroll
+  for (int i = 0; i < kQ8RowPer; ++i) {
+    const int c = i * kWave + lane;
+    const signed char qc = q8_quant(v[i], inv);
+    const float e = fmaf(-s, (float)qc, v[i]);
+    sq += (int)qc * (int)qc;
+    ee = fmaf(e, e, ee);
+    if (c < dq) dst[c] = c < d ? qc : (signed char)0;
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    sq += __shfl_xor(sq, off);
+    ee += __shfl_xor(ee, off);
+  }
+  if (lane == 0) {
+    float4 mt;
+    mt.x = s;
+    mt.y = s * sqrtf((float)sq) * kNormUp;
+    mt.z = sqrtf(ee) * kNormUp;
+    mt.w = 0.f;
+    *meta = mt;
+  }
+}
+
+}  // namespace cvs

@@ -68,12 +68,38 @@ struct Mfma<32> {
   __device__ static constexpr int row(int e) { return 8 * (e >> 2) + (e & 3); }
 };
 
+// int8 pre-filter: v_mfma_i32_32x32x32_i8.  Operands are the same 16 bytes per
+// lane as for 32x32x16_f16 (lane l: row l%32, bytes 16(l/32)..+15 of a 32-byte
+// k-step), so the kernel's byte addressing is unchanged: it runs on int8 rows
+// with d counted in 2-byte units.  Same D layout as Mfma<32>.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+struct MfmaI8 {
+  typedef int acc_t __attribute__((ext_vector_type(16)));
+  static constexpr int KSZ = 16;  // 2-byte units per k-step (32 int8)
+  static constexpr int NE = 16;
+  __device__ static acc_t run(half8 a, half8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b),
+                                                  c, 0, 0, 0);
+  }
+  __device__ static constexpr int row(int e) { return Mfma<32>::row(e); }
+};
+
+template <int MS, int MODE>
+struct MfmaFor {
+  typedef Mfma<MS> type;
+};
+template <>
+struct MfmaFor<32, kAppendQ8> {
+  typedef MfmaI8 type;
+};
+
 // FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
 // compile-time constant (per-stage guards on a runtime count split the
 // unrolled stage loop into separate blocks and cost ~15% of the scan).
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
 __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a) {
-  typedef Mfma<MS> M;
+  static_assert(MODE != kAppendQ8 || MS == 32, "int8 pre-filter uses the 32x32 MFMA");
+  typedef typename MfmaFor<MS, MODE>::type M;
   typedef typename M::acc_t acc_t;
   constexpr int RS = QS >= 4 ? 1 : 4 / QS;  // row splits
   constexpr int NW = QS * RS;       // waves: 4 (one per SIMD) or 8 (two per SIMD)
@@ -95,7 +121,8 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   constexpr bool PAIR = FULLW && (NCMAX % 2 == 0) && NBUF >= 5;
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
-  constexpr bool APP = (MODE == kAppend);
+  constexpr bool Q8 = (MODE == kAppendQ8);
+  constexpr bool APP = (MODE == kAppend || Q8);
   constexpr int STCAP = 64;          // staged entries per wave
   // A staged entry is one lane's NE scores of one (query block, row block): a
   // row of EST floats (NE plus padding to an odd number of 16-byte units, so
@@ -225,6 +252,13 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
     const int qi = qwave0 + qb * MS + col;
     thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
   }
+  // kAppendQ8: this lane's queries' (s_q, |q^|, |e|), for the score bound.
+  float4 qm[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    if (Q8) qm[qb] = a.qmeta[min(qwave0 + qb * MS + col, a.nq - 1)];
+    else qm[qb] = float4{0.f, 0.f, 0.f, 0.f};
+  }
   if (APP) {
     for (int i = tid; i < RS * BQ; i += NT) {
       (&lcnt[0][0])[i] = 0;
@@ -263,7 +297,8 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
       if (have) {
         const float tq = thr_s[rs][ql];
 #pragma unroll
-        for (int e = 0; e < M::NE; ++e) todo |= (ev[e] >= tq ? 1u : 0u) << e;
+        for (int e = 0; e < M::NE; ++e)  // (rows past n of the last tile are -inf: never appended)
+          todo |= (ev[e] >= tq && rbase + M::row(e) < n ? 1u : 0u) << e;
       }
 #pragma unroll 1
       while (true) {
@@ -280,6 +315,10 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
             ++put;
           }
         }
+        // int8 pre-filter: a full list is not compacted (its entries are only
+        // bounds); the surplus is dropped and the count, now above cap, marks
+        // the list as overflowed so that the select rescans its whole range.
+        if (Q8) todo = 0;
         uint64_t om = __ballot(todo != 0);
         if (!om) break;
 #pragma unroll 1
@@ -390,15 +429,37 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
     // ---- epilogue: acc[qb][rb][e] = score(query qwave0 + MS*qb + col,
     //                                        row rowb + MS*rb + M::row(e))
     const int64_t rowb = t * TR + rs * RW + 4 * kg;
+    // kAppendQ8: the meta of the 64-row block holding this wave's rows, read
+    // through the scalar cache (a vector load here would make the compiler wait
+    // for every outstanding stage load before using it).
+    float4 bm = float4{0.f, 0.f, 0.f, 0.f};
+    if (Q8) {
+      typedef const __attribute__((address_space(4))) float* cfloat_p;
+      // (a wave whose rows all lie past n, in the last tile, reads the last block)
+      const int64_t first = min(t * TR + rs * RW, n - 1);
+      const int blk = __builtin_amdgcn_readfirstlane((int)(first >> 6));
+      const cfloat_p m = (cfloat_p)a.bmeta + 4 * (int64_t)blk;
+      bm = float4{m[0], m[1], m[2], m[3]};
+    }
     const bool partial = (t * TR + TR > n);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
       float v[NV];
+      if (Q8) {  // upper bound of each exact score: A + slack
+        const float cq = qm[qb].x * bm.x;
+        const float slack = (fmaf(qm[qb].y, bm.y, qm[qb].z * bm.z) +
+                             a.gamma * (qm[qb].y + qm[qb].z) * (bm.y + bm.z)) * (1.0f + 1.0f / 1048576.0f);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = acc[qb][rb][e];
+          for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = fmaf((float)acc[qb][rb][e], cq, slack);
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = acc[qb][rb][e];
+      }
       if (partial) {  // only the corpus's last tile has rows past n
         const int64_t left = n - rowb;
 #pragma unroll
@@ -519,6 +580,14 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   }
 }
 
+// int8 pre-filter: full-width rows only (the int8 row bytes are padded to 32 * KS).
+template <int MS, int QS, int QB, int RB, int KS>
+hipError_t launch_one_q8(const ScanArgs& a, int grid, hipStream_t s) {
+  if (a.d != KS * MfmaI8::KSZ || a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendQ8, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   const bool full = (a.d == KS * Mfma<MS>::KSZ);
@@ -569,9 +638,30 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   X(32, 4, 1, 2, 48)        \
   X(32, 8, 1, 2, 24)
 
+// int8 pre-filter configurations (KS in 32-byte k-steps: 12, 24, 48 = int8 rows
+// of 384, 768, 1536 bytes).
+#define CVS_SCAN_Q8_CONFIGS(X) \
+  X(32, 1, 1, 1, 12)           \
+  X(32, 1, 1, 1, 24)           \
+  X(32, 1, 1, 1, 48)           \
+  X(32, 1, 2, 1, 12)           \
+  X(32, 1, 2, 1, 24)           \
+  X(32, 4, 1, 2, 12)           \
+  X(32, 4, 1, 2, 24)           \
+  X(32, 4, 1, 2, 48)           \
+  X(32, 8, 1, 2, 12)           \
+  X(32, 8, 1, 2, 24)
+
 }  // namespace
 
 bool scan_cfg_available(const ScanCfg& c, int mode) {
+  if (mode == kAppendQ8) {
+#define CVS_HAS_Q8(MS, QS, QB, RB, KS) \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return true;
+    CVS_SCAN_Q8_CONFIGS(CVS_HAS_Q8)
+#undef CVS_HAS_Q8
+    return false;
+  }
   if (mode < kAppend || mode > kStoreF16) return false;
 #define CVS_HAS(MS, QS, QB, RB, KS) \
   if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return true;
@@ -581,6 +671,14 @@ bool scan_cfg_available(const ScanCfg& c, int mode) {
 }
 
 hipError_t launch_scan(const ScanCfg& c, int mode, const ScanArgs& a, int grid, hipStream_t s) {
+  if (mode == kAppendQ8) {
+#define CVS_LAUNCH_Q8(MS, QS, QB, RB, KS)                                      \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) \
+    return launch_one_q8<MS, QS, QB, RB, KS>(a, grid, s);
+    CVS_SCAN_Q8_CONFIGS(CVS_LAUNCH_Q8)
+#undef CVS_LAUNCH_Q8
+    return hipErrorInvalidValue;
+  }
 #define CVS_LAUNCH(MS, QS, QB, RB, KS)                                              \
   if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) \
     return launch_one<MS, QS, QB, RB, KS>(mode, a, grid, s);

@@ -15,8 +15,16 @@
 // sampling pre-pass's unit maxima into per-query thresholds).  With one list
 // per query holding a whole score row it is also the row top-k of a score
 // matrix (k up to 1024: the large-k path).
+//
+// Rescore mode finishes the int8 pre-filter: list entries are row ids whose
+// score bound reached the threshold, and each one's exact score is recomputed
+// here from the fp16 rows (fp32 accumulation, v_dot2_f32_f16) before it enters
+// the selection.  A list that overflowed in the scan (count > cap) is replaced
+// by every row of its corpus range, so the result stays exact whatever the
+// data.
 #include "cvs_common.h"
 #include "cvs_kernels.h"
+#include "cvs_q8_row.h"
 
 namespace cvs {
 
@@ -131,20 +139,60 @@ __device__ void block_sort_desc(uint64_t* keys, int N) {
   }
 }
 
-template <int TAU_MODE>
+constexpr int kSelFinal = 0, kSelTau = 1, kSelRescore = 2, kSelRescoreWide = 3;
+constexpr int kMaxD = 1536;
+
+// Entries of list L of query q: its count, or in rescore mode the size of its
+// row range when it overflowed.
+__device__ __forceinline__ int list_len(const SelectArgs& a, int q, int L, bool rescore) {
+  if (!a.lcount) return a.cap;
+  const int c = a.lcount[(int64_t)q * a.nlists + L];
+  if (rescore && c > a.cap) return (int)(a.tpc * a.wave_rows);
+  return c;
+}
+
+// Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
+// l, l+16, ... (RL of them at most); each group works on RU candidates at once,
+// so RL*RU independent loads per lane are in flight.  RL = 4 covers d <= 512,
+// RL = 12 (one candidate at a time) d <= 1536.
+template <int MODE>
+struct RescoreShape {
+  static constexpr int RL = MODE == kSelRescoreWide ? 12 : 4;
+  static constexpr int RU = MODE == kSelRescoreWide ? 2 : 8;
+};
+
+template <int MODE>
 __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   __shared__ SelShared S;
+  constexpr bool RESCORE = (MODE == kSelRescore || MODE == kSelRescoreWide);
+  constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
+  __shared__ int sids[RESCORE ? kBatch : 1];  // a batch's candidate row ids (-1: none)
+  __shared__ unsigned ovf[RESCORE ? kSelectMaxLists / 32 : 1];  // overflowed-list bitmap
+  __shared__ int batch_ovf;  // the current batch holds rows of overflowed lists
   const int tid = threadIdx.x;
   const int q = blockIdx.x;
   const int NL = a.nlists;
   const int k = a.k;
+  const int l16 = tid & 15;
+  const int nd = RESCORE ? a.d / 8 : 0;  // 16-byte pieces per row
+  if (MODE == kSelTau && a.qq_out != nullptr && tid < kWave)  // int8 pre-filter: this query's int8 row
+    q8_query_row(a.q + (int64_t)q * a.d, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid);
+  half8 qv[RESCORE ? RL : 1];
+  if (RESCORE) {
+    const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
+#pragma unroll
+    for (int m = 0; m < RL; ++m) {
+      const int c = l16 + 16 * m;
+      qv[m] = c < nd ? qr[c] : half8{};
+    }
+  }
 
   // Exclusive prefix sum of the list counts.
   const int per = (NL + kBlock - 1) / kBlock;
   const int l0 = tid * per;
   const int l1 = min(NL, l0 + per);
   int sum = 0;
-  for (int L = l0; L < l1; ++L) sum += a.lcount ? a.lcount[(int64_t)q * NL + L] : a.cap;
+  for (int L = l0; L < l1; ++L) sum += list_len(a, q, L, RESCORE);
   S.part[tid] = sum;
   if (tid == 0) {
     S.nbuf = 0;
@@ -177,14 +225,25 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
     int run = S.part[tid];
     for (int L = l0; L < l1; ++L) {
       S.pre[L] = run;
-      run += a.lcount ? a.lcount[(int64_t)q * NL + L] : a.cap;
+      run += list_len(a, q, L, RESCORE);
     }
+  }
+  if (RESCORE) {
+    for (int i = tid; i < (NL + 31) / 32; i += kBlock) ovf[i] = 0u;
+    __syncthreads();
+    for (int L = tid; L < NL; L += kBlock)
+      if (a.lcount[(int64_t)q * NL + L] > a.cap) atomicOr(&ovf[L >> 5], 1u << (L & 31));
   }
   __syncthreads();
   const int total = S.pre[NL];
 
   for (int base = 0; base < total; base += kBatch) {
     const uint64_t t = S.thr_key;
+    if (RESCORE) {
+      __syncthreads();  // (everyone has read batch_ovf of the previous batch)
+      if (tid == 0) batch_ovf = 0;
+      __syncthreads();
+    }
     for (int j = 0; j < kBatch / kBlock; ++j) {
       const int gi = base + j * kBlock + tid;
       if (gi < total) {
@@ -195,9 +254,59 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
         }
         const int idx = gi - S.pre[lo];
         const int64_t off = ((int64_t)q * NL + lo) * a.cap + idx;
-        const int id = a.li ? a.li[off] : (int)((int64_t)lo * a.cap + idx);
-        const uint64_t key = make_key(a.lv[off], id);
-        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+        if (RESCORE) {
+          int id = -1;
+          if ((ovf[lo >> 5] >> (lo & 31)) & 1u) {  // overflowed: row idx of the list's range
+            const int64_t tile = (int64_t)(lo / a.rsplits) * a.tpc + idx / a.wave_rows;
+            const int64_t row = tile * a.tile_rows + (int64_t)(lo % a.rsplits) * a.wave_rows + idx % a.wave_rows;
+            id = (tile < a.ntiles && row < a.n) ? (int)row : -1;
+          } else {  // rescore_kernel has replaced the bound by the exact score
+            const int lid = a.li[off];
+            const uint64_t key = make_key(a.lv[off], lid);
+            if (lid >= 0 && lid < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+          }
+          sids[j * kBlock + tid] = id;
+          if (id >= 0) batch_ovf = 1;
+        } else {
+          const int id = a.li ? a.li[off] : (int)((int64_t)lo * a.cap + idx);
+          const uint64_t key = make_key(a.lv[off], id);
+          if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+        }
+      }
+    }
+    if (RESCORE) __syncthreads();
+    if (RESCORE && batch_ovf) {  // exact scores of the batch's overflow rows, 16 lanes per row
+      const int cnt = min(kBatch, total - base);
+      for (int c0 = (tid >> 4) * RU; c0 < cnt; c0 += (kBlock / 16) * RU) {
+        int idu[RU];
+        half8 xv[RU][RL];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) idu[u] = c0 + u < cnt ? sids[c0 + u] : -1;
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          const half8* xr = reinterpret_cast<const half8*>(a.x + (int64_t)(idu[u] < 0 ? 0 : idu[u]) * a.d);
+#pragma unroll
+          for (int m = 0; m < RL; ++m) {
+            const int c = l16 + 16 * m;
+            xv[u][m] = (idu[u] >= 0 && c < nd) ? xr[c] : half8{};
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < RL; ++m)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2)
+              acc = __builtin_amdgcn_fdot2(half2v{qv[m][j], qv[m][j + 1]}, half2v{xv[u][m][j], xv[u][m][j + 1]}, acc,
+                                           false);
+#pragma unroll
+          for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+          if (l16 == 0 && idu[u] >= 0) {
+            const uint64_t key = make_key(acc, idu[u]);
+            if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+          }
+        }
       }
     }
     __syncthreads();
@@ -214,7 +323,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
 
   const int nb = min(S.nbuf, k);
-  if (TAU_MODE) {
+  if (MODE == kSelTau) {
     // the k-th best key is the smallest survivor
     if (tid < kWave) {
       uint64_t m = ~0ull;
@@ -239,6 +348,119 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
         ((int*)a.out_i)[(int64_t)q * k + r] = id;
     }
   }
+}
+
+// Exact scores of the int8 pre-filter's candidates, written over their bounds
+// in lv: workgroup b takes query b / splits and its lists [s*lpb, (s+1)*lpb),
+// s = b % splits.  Overflowed lists (count > cap) are left to the select.
+// Then each list is compacted to the candidates that can still be in the top
+// k: with tau the k-th best fp32 score of the sampled rows and eps >= the
+// rounding error of any fp32 sum of a row's d products (d * 2^-24 * |q| |x|),
+// the k-th best exact score over all rows is >= tau - 2 eps, so a candidate
+// below that can never be returned.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
+  constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
+  __shared__ int pre[kBlock + 1];
+  __shared__ int wsum[kWaves];
+  __shared__ int kept[kBlock];      // survivors per list so far
+  __shared__ int sid[kBatch];       // a batch's candidate ids
+  __shared__ short slist[kBatch];   // ... and their lists (local index)
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int l16 = tid & 15;
+  const int NL = a.nlists;
+  const int splits = (NL + a.lpb - 1) / a.lpb;
+  const int q = blockIdx.x / splits;
+  const int L0 = (blockIdx.x % splits) * a.lpb;
+  const int nl = min(a.lpb, NL - L0);
+  int c = 0;
+  if (tid < nl) {
+    c = a.lcount[(int64_t)q * NL + L0 + tid];
+    if (c > a.cap) c = 0;  // overflowed: left to the select
+  }
+  kept[tid] = 0;
+  int v = c;  // inclusive scan of the list counts
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int o = __shfl_up(v, off);
+    if (lane >= off) v += o;
+  }
+  if (lane == kWave - 1) wsum[tid / kWave] = v;
+  __syncthreads();
+  for (int i = 0; i < tid / kWave; ++i) v += wsum[i];
+  pre[tid + 1] = v;
+  if (tid == 0) pre[0] = 0;
+  __syncthreads();
+  const int total = pre[nl];
+  float cut = -__builtin_inff();
+  if (a.tau_in) {  // tau - 2 eps, eps = gamma |q| max|x| (the sampled rows' norms are <= max|x|)
+    const float4 qm = a.qmeta[q];
+    cut = a.tau_in[q] - (qm.y + qm.z) * a.xmax[0] * 2.f * a.gamma * (1.0f + 1.0f / 1024.0f);
+  }
+  const int nd = a.d / 8;
+  const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
+  half8 qv[RL];
+#pragma unroll
+  for (int m = 0; m < RL; ++m) {
+    const int cc = l16 + 16 * m;
+    qv[m] = cc < nd ? qr[cc] : half8{};
+  }
+  float* lvq = const_cast<float*>(a.lv) + ((int64_t)q * NL + L0) * a.cap;
+  int* liq = const_cast<int*>(a.li) + ((int64_t)q * NL + L0) * a.cap;
+  for (int base = 0; base < total; base += kBatch) {
+    const int cnt = min(kBatch, total - base);
+    // every id of the batch is read before any survivor is written back, and a
+    // survivor's new slot never passes an unread entry of its list
+    for (int i = tid; i < cnt; i += kBlock) {
+      const int gi = base + i;
+      int lo = 0, hi = nl;  // largest list with pre[list] <= gi
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= gi) lo = mid; else hi = mid;
+      }
+      const int id = liq[(int64_t)lo * a.cap + (gi - pre[lo])];
+      sid[i] = (id >= 0 && id < a.n) ? id : -1;
+      slist[i] = (short)lo;
+    }
+    __syncthreads();
+    for (int c0 = (tid >> 4) * RU; c0 < cnt; c0 += (kBlock / 16) * RU) {
+      int idu[RU];
+      half8 xv[RU][RL];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) idu[u] = c0 + u < cnt ? sid[c0 + u] : -1;
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const half8* xr = reinterpret_cast<const half8*>(a.x + (int64_t)(idu[u] < 0 ? 0 : idu[u]) * a.d);
+#pragma unroll
+        for (int m = 0; m < RL; ++m) {
+          const int cc = l16 + 16 * m;
+          xv[u][m] = (idu[u] >= 0 && cc < nd) ? xr[cc] : half8{};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < RL; ++m)
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            acc = __builtin_amdgcn_fdot2(half2v{qv[m][j], qv[m][j + 1]}, half2v{xv[u][m][j], xv[u][m][j + 1]},
+                                         acc, false);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+        if (l16 == 0 && idu[u] >= 0 && acc >= cut) {
+          const int lo = slist[c0 + u];
+          const int pos = atomicAdd(&kept[lo], 1);
+          lvq[(int64_t)lo * a.cap + pos] = acc;
+          liq[(int64_t)lo * a.cap + pos] = idu[u];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < nl && a.lcount[(int64_t)q * NL + L0 + tid] <= a.cap)
+    const_cast<int*>(a.lcount)[(int64_t)q * NL + L0 + tid] = kept[tid];
 }
 
 // Exact top-k of one chunk of one score row: workgroup b takes row b / chunks,
@@ -327,12 +549,44 @@ hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_select(int tau_mode, const SelectArgs& a, int nq, hipStream_t s) {
-  if (a.nlists < 1 || a.nlists > kSelectMaxLists || a.k < 1 || a.k > kSelectMaxK) return hipErrorInvalidValue;
-  if (tau_mode)
-    hipLaunchKernelGGL(select_kernel<1>, dim3(nq), dim3(kBlock), 0, s, a);
+hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s) {
+  if (a.q == nullptr || a.x == nullptr || a.li == nullptr || a.lv == nullptr || a.lcount == nullptr || a.d < 8 ||
+      a.d % 8 != 0 || a.d > kMaxD || a.lpb < 1 || a.lpb > kBlock || a.nlists < 1)
+    return hipErrorInvalidValue;
+  const int64_t grid = (int64_t)nq * ((a.nlists + a.lpb - 1) / a.lpb);
+  if (grid < 1 || grid > 0x7fffffff) return hipErrorInvalidValue;
+  if (a.d <= 16 * 8 * RescoreShape<kSelRescore>::RL)
+    hipLaunchKernelGGL(rescore_kernel<kSelRescore>, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
   else
-    hipLaunchKernelGGL(select_kernel<0>, dim3(nq), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(rescore_kernel<kSelRescoreWide>, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
+  if (a.nlists < 1 || a.nlists > kSelectMaxLists || a.k < 1 || a.k > kSelectMaxK) return hipErrorInvalidValue;
+  switch (mode) {
+    case kSelFinal:
+      hipLaunchKernelGGL(select_kernel<kSelFinal>, dim3(nq), dim3(kBlock), 0, s, a);
+      break;
+    case kSelTau:
+      if (a.qq_out != nullptr &&
+          (a.q == nullptr || a.qmeta_out == nullptr || a.d < 1 || a.d > a.dq || a.dq > kQ8RowPer * kWave))
+        return hipErrorInvalidValue;
+      hipLaunchKernelGGL(select_kernel<kSelTau>, dim3(nq), dim3(kBlock), 0, s, a);
+      break;
+    case kSelRescore:
+      if (a.q == nullptr || a.x == nullptr || a.li == nullptr || a.lcount == nullptr || a.d < 8 || a.d % 8 != 0 ||
+          a.d > kMaxD || a.wave_rows < 1 || a.rsplits < 1 || a.tile_rows < a.rsplits * a.wave_rows ||
+          (int64_t)a.tpc * a.wave_rows > 0x7fffffff)
+        return hipErrorInvalidValue;
+      if (a.d <= 16 * 8 * RescoreShape<kSelRescore>::RL)
+        hipLaunchKernelGGL(select_kernel<kSelRescore>, dim3(nq), dim3(kBlock), 0, s, a);
+      else
+        hipLaunchKernelGGL(select_kernel<kSelRescoreWide>, dim3(nq), dim3(kBlock), 0, s, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -76,6 +76,18 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.cvs_fused_topk_marked.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                           vp, vp, ctypes.POINTER(i64), i32, vp,
                                           ctypes.POINTER(vp)]
+    lib.cvs_q8_corpus_bytes.restype = i32
+    lib.cvs_q8_corpus_bytes.argtypes = [i64, i64, ctypes.POINTER(i64)]
+    lib.cvs_q8_build.restype = i32
+    lib.cvs_q8_build.argtypes = [vp, i64, i64, vp, i64, i32, vp]
+    lib.cvs_q8_plan.restype = i32
+    lib.cvs_q8_plan.argtypes = [i64, i64, i64, i64, i32, i32, ctypes.POINTER(i64), ctypes.POINTER(i64)]
+    lib.cvs_q8_topk.restype = i32
+    lib.cvs_q8_topk.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i64, vp, vp,
+                                ctypes.POINTER(i64), i32, vp]
+    lib.cvs_q8_topk_marked.restype = i32
+    lib.cvs_q8_topk_marked.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i64, vp, vp,
+                                       ctypes.POINTER(i64), i32, vp, ctypes.POINTER(vp)]
     return lib
 
 
@@ -249,6 +261,76 @@ class Engine:
             rc = self.lib.cvs_fused_topk(*args)
         else:
             rc = self.lib.cvs_fused_topk_timed(*args, stage_ms)
+        if rc != 0:
+            raise self._error(rc)
+        return [out_v, out_i, plan]
+
+
+    # -- int8 pre-filter (no counterpart in the reference) ------------------------
+    def q8_corpus_bytes(self, n: int, d: int) -> int:
+        out = ctypes.c_int64(0)
+        rc = self.lib.cvs_q8_corpus_bytes(int(n), int(d), ctypes.byref(out))
+        if rc != 0:
+            raise self._error(rc)
+        return int(out.value)
+
+    def q8_build(self, x):
+        """int8 companion of the fp16 corpus ``x`` (a uint8 tensor on its device)."""
+        import torch
+
+        self._check_matrix(x, "corpus")
+        n, d = x.shape
+        xq = torch.empty(self.q8_corpus_bytes(n, d), dtype=torch.uint8, device=x.device)
+        rc = self.lib.cvs_q8_build(x.data_ptr(), n, d, xq.data_ptr(), xq.numel(), x.device.index,
+                                   self._stream(x.device))
+        if rc != 0:
+            raise self._error(rc)
+        return xq
+
+    def q8_plan(self, nq: int, n: int, d: int, k: int, flags: int = 0, device: int = 0):
+        plan = (ctypes.c_int64 * 2)()
+        ws = ctypes.c_int64(0)
+        rc = self.lib.cvs_q8_plan(nq, n, d, k, flags, device, plan, ctypes.byref(ws))
+        if rc != 0:
+            raise self._error(rc)
+        return [int(plan[0]), int(plan[1])], int(ws.value)
+
+    def q8_topk(self, q, x, xq, k: int, flags: int = 0, marks=None):
+        """Exact top-k through the int8 pre-filter; same results as fused_topk.
+        ``xq`` is ``q8_build(x)``.  With ``marks`` (five timing-enabled events)
+        the stages are marked as in fused_topk_marked."""
+        import torch
+
+        self._check_pair(q, x)
+        if not (isinstance(xq, torch.Tensor) and xq.dtype == torch.uint8 and xq.device == x.device
+                and xq.is_contiguous()):
+            raise RuntimeError("xq must be the contiguous uint8 tensor q8_build returned, on the corpus's device")
+        nq, d = q.shape
+        n = x.shape[0]
+        k = int(k)
+        dev = q.device
+        plan_c = (ctypes.c_int64 * 2)()
+        ws_bytes = ctypes.c_int64(0)
+        rc = self.lib.cvs_q8_plan(nq, n, d, k, flags, dev.index, plan_c, ctypes.byref(ws_bytes))
+        if rc != 0:
+            raise self._error(rc)
+        out_v = torch.empty((nq, k), dtype=torch.float32, device=dev)
+        out_i = torch.empty((nq, k), dtype=torch.int64 if flags & FLAG_IDS_INT64 else torch.int32, device=dev)
+        plan = torch.tensor([int(plan_c[0]), int(plan_c[1])], dtype=torch.int64)
+        if nq == 0:
+            return [out_v, out_i, plan]
+        ws = torch.empty(max(int(ws_bytes.value), 256), dtype=torch.uint8, device=dev)
+        args = (q.data_ptr(), x.data_ptr(), xq.data_ptr(), xq.numel(), nq, n, d, k, flags, ws.data_ptr(),
+                ws.numel(), out_v.data_ptr(), out_i.data_ptr(), plan_c, dev.index, self._stream(dev))
+        if marks is not None:
+            if len(marks) != 5:
+                raise ValueError("marks must hold 5 events")
+            for ev in marks:
+                if not ev.cuda_event:
+                    ev.record()
+            rc = self.lib.cvs_q8_topk_marked(*args, (ctypes.c_void_p * 5)(*[ev.cuda_event for ev in marks]))
+        else:
+            rc = self.lib.cvs_q8_topk(*args)
         if rc != 0:
             raise self._error(rc)
         return [out_v, out_i, plan]

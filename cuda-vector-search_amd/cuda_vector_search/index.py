@@ -25,8 +25,32 @@ MAX_EXACT_K = 1024  # largest k of the exact large-k path (score matrix + row to
 _SCORE_BLOCK_BYTES = 1 << 31  # fp32 score rows computed per block on the large-k path
 MAX_KERNEL_WIDTH = 1536  # widest (padded) rows the gfx950 kernels accept
 _NORM_CHUNK = 1 << 18
+# int8 pre-filter (an int8 companion of the corpus scanned instead of the fp16
+# rows; exact results).  Built by default for corpora of at least Q8_MIN_ROWS
+# rows wider than Q8_MIN_WIDTH; "auto" uses it where it measured faster than the
+# fp16 scan: batch 1 (bandwidth-bound GEMV on half the bytes), and batches with
+# k <= Q8_MAX_K over at least Q8_BATCH_MIN_ROWS rows.
+Q8_MIN_ROWS = 1 << 18
+Q8_MIN_WIDTH = 256
+Q8_MAX_K = 16
+Q8_BATCH_MIN_ROWS = 1 << 19
 
-METHODS = ("auto", "fused", "twopass", "torch")
+METHODS = ("auto", "fused", "twopass", "torch", "int8")
+
+
+def int8_builds(n: int, width: int) -> bool:
+    """Whether Index builds the int8 companion by default (int8_prefilter=None)."""
+    return n >= Q8_MIN_ROWS and Q8_MIN_WIDTH < width <= MAX_KERNEL_WIDTH
+
+
+def int8_auto(n: int, width: int, nq: int, k: int) -> bool:
+    """Whether method="auto" runs the int8 path (default companion, k <= 256)."""
+    return int8_builds(n, width) and k <= MAX_FUSED_K and (nq == 1 or (k <= Q8_MAX_K and n >= Q8_BATCH_MIN_ROWS))
+
+
+def q8_row_bytes(width: int) -> int:
+    """Bytes of one int8 companion row (the smallest int8 scan width >= width)."""
+    return 384 if width <= 384 else 768 if width <= 768 else 1536
 
 
 def _as_tensor(a) -> torch.Tensor:
@@ -59,9 +83,15 @@ class Index:
         device: ``"cuda"``, ``"cuda:1"``, ``"cpu"``...; defaults to the GPU when present.
         copy: with ``False`` a contiguous fp16 tensor already on the device is stored
             without a copy (and normalised in place for cosine).
+        int8_prefilter: build the int8 companion used by ``method="int8"`` (and by
+            "auto" where it is faster): None = when the corpus is large enough
+            (>= 2^18 rows wider than 256), True = always on a gfx950 GPU, False =
+            never.  It holds one byte per stored element, built once here; like
+            the normalisation, it reflects the corpus at construction.
     """
 
-    def __init__(self, embeddings, metric: str = "cosine", device=None, copy: bool = True):
+    def __init__(self, embeddings, metric: str = "cosine", device=None, copy: bool = True,
+                 int8_prefilter: bool | None = None):
         if metric not in ("cosine", "ip"):
             raise ValueError("metric must be 'cosine' or 'ip'")
         src = _as_tensor(embeddings)
@@ -96,6 +126,10 @@ class Index:
             if metric == "cosine":
                 _normalize_(x)
             self._x = _padded(x) if on_gpu else x
+        self._xq = None
+        if self._use_kernels and self._x.shape[1] <= MAX_KERNEL_WIDTH and int8_prefilter is not False:
+            if int8_prefilter or int8_builds(self._x.shape[0], self._x.shape[1]):
+                self._xq = _ext.load().q8_build(self._x)
 
     # -- basics -------------------------------------------------------------
     def __len__(self) -> int:
@@ -132,8 +166,12 @@ class Index:
             "fused"   - gfx950 engine: MFMA scores + threshold filter + exact select (k <= 256)
             "twopass" - gfx950 score kernel writes the fp16 matrix, then torch.topk
             "torch"   - torch matmul + torch.topk
-            "auto"    - fused for k <= 256; exact fp32 scores + row top-k for k <= 1024;
-                        else torch
+            "int8"    - gfx950 engine over the int8 companion: int8 scan/GEMV with a
+                        rigorous error bound, exact fp16 rescoring of what passes
+                        (same results as "fused", k <= 256)
+            "auto"    - int8 where it is faster (batch 1, or k <= 16 over >= 2^19
+                        rows), else fused, for k <= 256; exact fp32 scores + row
+                        top-k for k <= 1024; else torch
         """
         if method not in METHODS:
             raise ValueError(f"method must be one of {METHODS}")
@@ -145,13 +183,20 @@ class Index:
         if method == "auto":
             width_ok = self._use_kernels and self._x.shape[1] <= MAX_KERNEL_WIDTH
             if width_ok and k <= MAX_FUSED_K:
-                method = "fused"
+                method = "int8" if self._int8_wins(q.shape[0], k) else "fused"
             elif width_ok and k <= MAX_EXACT_K:
                 return self._search_large_k(q, k)
             else:
                 method = "torch"
-        if method in ("fused", "twopass") and not self._use_kernels:
+        if method in ("fused", "twopass", "int8") and not self._use_kernels:
             raise RuntimeError(f"method={method!r} needs an AMD Instinct MI355X (gfx950) GPU")
+        if method == "int8":
+            if k > MAX_FUSED_K:
+                raise ValueError(f"int8 search supports k <= {MAX_FUSED_K}")
+            if self._xq is None:
+                self._xq = _ext.load().q8_build(self._x)
+            v, i, _ = _ext.load().q8_topk(q, self._x, self._xq, k, flags=_ext.FLAG_IDS_INT64)
+            return v, i
         if method == "fused":
             if k > MAX_FUSED_K:
                 raise ValueError(f"fused search supports k <= {MAX_FUSED_K}")
@@ -163,6 +208,12 @@ class Index:
             v, i = torch.topk(s, k, dim=1)
             return v.float(), i
         return torch_topk(q, self._x, k)
+
+    def _int8_wins(self, nq: int, k: int) -> bool:
+        """Whether "auto" sends a batch of nq queries with this k to the int8 path."""
+        if self._xq is None:
+            return False
+        return nq == 1 or (k <= Q8_MAX_K and len(self) >= Q8_BATCH_MIN_ROWS)
 
     def _search_large_k(self, q: torch.Tensor, k: int):
         """Exact top-k for MAX_FUSED_K < k <= MAX_EXACT_K on the GPU: fp32 score

@@ -153,6 +153,40 @@ int cvs_topk_rows_plan(int64_t nq, int64_t n, int64_t k, int device, int64_t* wo
 int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_stride, int64_t dst_width,
                   int normalize, int device, void* stream);
 
+/*
+ * int8 pre-filter for the exact search (no counterpart in the reference, whose
+ * only corpus format is the fp16 matrix of index.py:56-78; it serves the same
+ * calls as cvs_fused_topk, index.py:123-126, with half the corpus bytes
+ * scanned).  An int8 companion of the corpus, built once, is scanned with int8
+ * MFMAs; every row whose score upper bound (int8 score + a rigorous
+ * quantisation-error bound) reaches the sampled threshold is kept, and the
+ * select kernel recomputes those rows' exact fp16 scores.  Results are those of
+ * cvs_fused_topk (same order, same ids, fp32-accumulated scores).
+ *
+ * cvs_q8_corpus_bytes: size of the companion of an [n, d] corpus (int8 rows of
+ *   384, 768 or 1536 bytes, the smallest that holds d, plus 16 bytes per
+ *   64-row block and 16 bytes for the corpus-wide maximum row norm).
+ * cvs_q8_build: writes the companion of x (d multiple of 64, <= 1536) into xq
+ *   (256-byte aligned, at least cvs_q8_corpus_bytes).  Rebuild it whenever x
+ *   changes.
+ * cvs_q8_plan / cvs_q8_topk: as cvs_fused_plan / cvs_fused_topk (1 <= k <= 256,
+ *   auto plan only; flags CVS_FLAG_IDS_INT64, and the pre-pass flags for the
+ *   sampling pass), with the companion of x as xq.  plan_out[0] is the int8
+ *   scan's query block, plan_out[1] its corpus chunks.
+ * cvs_q8_topk_marked: as cvs_fused_topk_marked (events around: query
+ *   quantisation + sampling pass, threshold select, int8 scan, rescore select).
+ */
+int cvs_q8_corpus_bytes(int64_t n, int64_t d, int64_t* bytes);
+int cvs_q8_build(const void* x, int64_t n, int64_t d, void* xq, int64_t xq_bytes, int device, void* stream);
+int cvs_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int device, int64_t* plan_out,
+                int64_t* workspace_bytes);
+int cvs_q8_topk(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64_t nq, int64_t n, int64_t d,
+                int64_t k, int flags, void* workspace, int64_t workspace_bytes, float* out_v, void* out_i,
+                int64_t* plan_out, int device, void* stream);
+int cvs_q8_topk_marked(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64_t nq, int64_t n,
+                       int64_t d, int64_t k, int flags, void* workspace, int64_t workspace_bytes, float* out_v,
+                       void* out_i, int64_t* plan_out, int device, void* stream, void* const* marks);
+
 #ifdef __cplusplus
 }
 #endif

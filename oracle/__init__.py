@@ -19,6 +19,12 @@ Contents, each restating one reference function (file:line into the reference):
   argpartition + argsort), used as a CPU baseline.
 * ``normalize_rows``     - ``index.py:35-41`` + ``index.py:27-32`` (cosine
   normalisation and zero-padding of fp16 rows).
+* ``q8_quantize_blocks`` / ``q8_quantize_queries`` / ``q8_bound`` - the int8
+  pre-filter's data format (this build's own design; no reference counterpart):
+  symmetric int8 rows with one scale per 64-row corpus block or per query, and
+  the Cauchy-Schwarz bound |q.x - A| <= |q^| |f| + |e| |x| that keeps the
+  pre-filter exact.  Pinned by closed forms (scales, saturation, ties-to-even)
+  and by the bound holding, and failing without either term, on random data.
 * ``check_exact``        - the acceptance rule of ``tests/test_search.py:21-44``
   plus the id-parity rule (ids identical except inside the near-tie band of the
   k-th score).
@@ -194,6 +200,84 @@ def normalize_rows(x, width: int | None = None, normalize: bool = True) -> np.nd
     out = np.zeros((n, width), dtype=np.float16)
     out[:, :d] = f.astype(np.float16)
     return out
+
+
+def q8_row_bytes(d: int) -> int:
+    """int8 row bytes for fp16 rows of width d: 384, 768 or 1536."""
+    return 384 if d <= 384 else 768 if d <= 768 else 1536
+
+
+def _q8_rows(f32: np.ndarray):
+    """Quantise rows sharing one scale: s = fp32(max|x|) / 127 and
+    x~ = clip(rint(x * fp32(127 / max)), -127, 127), all in fp32 (rint ties to
+    even), as the GPU kernels do.  Returns (x~ as float64, s)."""
+    m = np.float32(np.abs(f32).max()) if f32.size else np.float32(0)
+    s = np.float32(m / np.float32(127))
+    inv = np.float32(np.float32(127) / m) if m > 0 else np.float32(0)
+    qv = np.clip(np.rint(f32 * inv), -127, 127)
+    return qv.astype(np.float64), s
+
+
+def q8_quantize_blocks(x, block: int = 64):
+    """int8 companion of an fp16 corpus (``cvs_q8.hip`` ``q8_build_kernel``).
+
+    Returns ``(xq, meta)``: ``xq`` int8 ``[ceil(n/64)*64, q8_row_bytes(d)]`` (zero
+    padding columns and rows) and ``meta`` float64 ``[ceil(n/64), 3]`` = (block
+    scale s_b as the fp32 value the GPU stores, exact max_r |f_r|_2, exact
+    max_r |x_r|_2) with f_r = x_r - s_b x~_r.  The GPU stores the two norms
+    rounded up; a test checks they are >= these and within 0.2%."""
+    x16 = _as_half(x)
+    n, d = x16.shape
+    dq = q8_row_bytes(d)
+    nblk = -(-n // block)
+    xq = np.zeros((nblk * block, dq), dtype=np.int8)
+    meta = np.zeros((nblk, 3), dtype=np.float64)
+    xf = x16.astype(np.float32)
+    for b in range(nblk):
+        rows = xf[b * block:(b + 1) * block]
+        qv, s = _q8_rows(rows)
+        xq[b * block:b * block + rows.shape[0], :d] = qv.astype(np.int8)
+        f = rows.astype(np.float64) - np.float64(s) * qv
+        meta[b, 0] = s
+        meta[b, 1] = np.sqrt((f * f).sum(axis=1)).max()
+        meta[b, 2] = np.sqrt((rows.astype(np.float64) ** 2).sum(axis=1)).max()
+    return xq, meta
+
+
+def q8_quantize_queries(q):
+    """Per-row int8 queries (``q8_query_kernel``): ``(qq, meta)`` with ``qq`` int8
+    ``[nq, q8_row_bytes(d)]`` and ``meta`` float64 ``[nq, 3]`` = (s_q as stored,
+    exact |q^|_2 = s_q |q~|_2, exact |e|_2 with e = q - q^)."""
+    q16 = _as_half(q)
+    nq, d = q16.shape
+    dq = q8_row_bytes(d)
+    qq = np.zeros((nq, dq), dtype=np.int8)
+    meta = np.zeros((nq, 3), dtype=np.float64)
+    qf = q16.astype(np.float32)
+    for r in range(nq):
+        qv, s = _q8_rows(qf[r])
+        qq[r, :d] = qv.astype(np.int8)
+        e = qf[r].astype(np.float64) - np.float64(s) * qv
+        meta[r] = (s, np.float64(s) * np.sqrt((qv * qv).sum()), np.sqrt((e * e).sum()))
+    return qq, meta
+
+
+def q8_bound(q, x, block: int = 64):
+    """(A, B, S): the int8 estimate A = s_q s_b sum(q~ x~), the bound B =
+    |q^| |f_r| + |e| |x_r| (per row, exact), and the exact scores S = q.x in
+    float64, for every (query, row) pair."""
+    x16, q16 = _as_half(x), _as_half(q)
+    n, d = x16.shape
+    xq, _ = q8_quantize_blocks(x16, block)
+    qq, qm = q8_quantize_queries(q16)
+    xs = np.repeat(q8_quantize_blocks(x16, block)[1][:, 0], block)[:n]
+    xf = x16.astype(np.float64)
+    xt = xq[:n, :d].astype(np.float64)
+    A = (qq[:, :d].astype(np.float64) @ xt.T) * qm[:, :1] * xs[None, :]
+    f = xf - xs[:, None] * xt
+    B = qm[:, 1:2] * np.sqrt((f * f).sum(axis=1))[None, :] + qm[:, 2:3] * np.sqrt((xf * xf).sum(axis=1))[None, :]
+    S = q16.astype(np.float64) @ xf.T
+    return A, B, S
 
 
 class ParityError(AssertionError):

@@ -22,17 +22,32 @@ def test_dominant_kernel_patterns_match_the_append_launches_only():
     assert gemv.search("void cvs::(anonymous namespace)::gemv_kernel<12, 0>(cvs::GemvArgs)")
     assert not gemv.search("void cvs::(anonymous namespace)::gemv_kernel<12, 1>(cvs::GemvArgs)")
     assert bench.COPY_KERNEL.search("__amd_rocclr_copyBuffer")
+    scan8 = bench.DOMINANT["scan_q8"]
+    assert scan8.search("void cvs::(anonymous namespace)::scan_kernel<32, 8, 1, 2, 12, 4, true>(cvs::ScanArgs)")
+    assert not scan8.search("void cvs::(anonymous namespace)::scan_kernel<32, 8, 1, 2, 24, 1, true>(cvs::ScanArgs)")
+    gemv8 = bench.DOMINANT["gemv_q8"]
+    assert gemv8.search("void cvs::(anonymous namespace)::gemv_kernel<6, 4>(cvs::GemvArgs)")
+    assert not gemv8.search("void cvs::(anonymous namespace)::gemv_kernel<12, 1>(cvs::GemvArgs)")
+
+
+def test_dominant_kernel_follows_the_auto_path():
+    # C2 (1M x 384, b256, k10) and C3 (b1) take the int8 pre-filter; C1 (100k
+    # rows), C4 and C5 (k=100) the fp16 fused path
+    assert [bench.dominant_key(c) for c in ("C1", "C2", "C3", "C4", "C5")] == \
+        ["scan", "scan_q8", "gemv_q8", "scan", "scan"]
 
 
 def test_instantiated_kernels_are_the_ones_the_patterns_expect():
     src = (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_scan.hip").read_text()
     assert "template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>" in src
-    assert "kAppend = 0," in (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_kernels.h").read_text()
+    hdr = (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_kernels.h").read_text()
+    assert "kAppend = 0," in hdr and "kAppendQ8 = 4," in hdr
 
 
 def test_algorithmic_bytes():
     assert bench.kernel_bytes(1_000_000, 384, 256) == 2 * 1_000_000 * 384 + 2 * 256 * 384
     assert bench.kernel_bytes(4_000_000, 768, 1) == 6_144_001_536
+    assert bench.kernel_bytes_q8(1_000_000, 384, 256) == 384_000_000 + 256 * 384
 
 
 def test_more_than_one_gpu_is_refused_with_a_message():

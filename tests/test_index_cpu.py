@@ -30,7 +30,9 @@ def make(n, d, b, seed=0, normal=True):
 def test_public_surface():
     assert __version__ == "0.1.0"
     assert callable(exact_topk_fp32) and callable(torch_topk)
-    assert index_mod.METHODS == ("auto", "fused", "twopass", "torch")
+    # the reference's methods (index.py:104-131), plus the int8 pre-filter
+    assert index_mod.METHODS[:4] == ("auto", "fused", "twopass", "torch")
+    assert index_mod.METHODS[4:] == ("int8",)
     assert index_mod.PAD == 64 and index_mod.MAX_FUSED_K == 256
 
 

@@ -198,3 +198,66 @@ def test_normalize_rows_agrees_with_the_torch_restatement():
     o = oracle.normalize_rows(x)
     ulp = np.maximum(np.abs(np.spacing(o)), np.abs(np.spacing(t))).astype(np.float32)
     assert np.all(np.abs(t.astype(np.float32) - o.astype(np.float32)) <= ulp)
+
+
+# --------------------------------------------------------------------------- int8 pre-filter format
+
+
+def test_q8_quantisation_closed_forms():
+    # block max 127 -> scale exactly 1: integers stay, halves round to even
+    x = np.zeros((3, 64), dtype=np.float16)
+    x[0, 0] = 127
+    x[0, 1:7] = [2.5, 3.5, -2.5, -0.5, 126.5, 1.25]
+    x[1, :] = -127                      # saturates exactly, zero residual
+    xq, meta = oracle.q8_quantize_blocks(x)
+    assert xq.shape == (64, 384) and xq.dtype == np.int8
+    assert xq[0, :7].tolist() == [127, 2, 4, -2, 0, 126, 1]
+    assert (xq[1, :64] == -127).all() and (xq[2] == 0).all() and (xq[3:] == 0).all()
+    assert (xq[:, 64:] == 0).all()      # zero padding columns
+    assert meta[0, 0] == 1.0
+    # residual: row 0 keeps 0.5, 0.5, 0.5, 0.5, 0.5, 0.25 away from the grid
+    assert np.isclose(meta[0, 1], np.sqrt(5 * 0.25 + 0.0625))
+    assert meta[0, 2] == 127 * 8          # the largest row norm of the block (row 1)
+    # an all-zero block has scale 0 and no residual
+    z, zm = oracle.q8_quantize_blocks(np.zeros((10, 128), dtype=np.float16))
+    assert (z == 0).all() and (zm == 0).all()
+    # queries: one scale per row
+    q = np.array([[127, 63.5, -1], [0.5, 0.25, 0]], dtype=np.float16)
+    q = np.pad(q, ((0, 0), (0, 61)))
+    qq, qm = oracle.q8_quantize_queries(q)
+    assert qq[0, :3].tolist() == [127, 64, -1]   # 63.5 -> 64 (even)
+    assert qq[1, :2].tolist() == [127, 64]        # scale 0.5/127: 0.25 -> 63.5 -> 64
+    assert qm[0, 0] == 1.0 and np.isclose(qm[0, 2], 0.5)
+    assert np.isclose(qm[1, 0], np.float32(np.float32(0.5) / np.float32(127)))
+
+
+def test_q8_bound_holds_and_needs_both_terms():
+    rng = np.random.default_rng(5)
+    # random rows of mixed scales, including heavy-tailed ones
+    x = (rng.standard_normal((512, 384)) * rng.uniform(0.01, 3, (512, 1))).astype(np.float16)
+    x[::7, rng.integers(0, 384)] *= 40
+    q = rng.standard_normal((9, 384)).astype(np.float16)
+    A, B, S = oracle.q8_bound(q, x)
+    assert (np.abs(S - A) <= B).all()
+    # a query that is exactly representable (integers, max 127: e = 0) and
+    # aligned with a row's residual f: |S - A| = |q.f| reaches |q^||f|, so the
+    # bound without its f-term (|e||x| = 0) fails
+    xq, meta = oracle.q8_quantize_blocks(x)
+    f = x[0].astype(np.float64) - meta[0, 0] * xq[0, :384].astype(np.float64)
+    qa = np.rint(127 * f / np.abs(f).max()).astype(np.float16)[None, :]
+    A, B, S = oracle.q8_bound(qa, x[:64])
+    _, qm = oracle.q8_quantize_queries(qa)
+    assert qm[0, 2] == 0.0 and (np.abs(S - A) <= B).all()
+    assert abs(S[0, 0] - A[0, 0]) > 0.5 * B[0, 0]
+    without_f = qm[0, 2] * np.sqrt((x[:64].astype(np.float64) ** 2).sum(axis=1))
+    assert (np.abs(S - A)[0] > without_f).any()
+    # a row that is exactly representable (f = 0) and aligned with a query's
+    # residual e: the bound without its e-term (|q^||f| = 0) fails
+    qb = rng.standard_normal((1, 384)).astype(np.float16)
+    qq, qm = oracle.q8_quantize_queries(qb)
+    e = qb[0].astype(np.float64) - qm[0, 0] * qq[0, :384].astype(np.float64)
+    xb = np.rint(127 * e / np.abs(e).max()).astype(np.float16)[None, :]
+    A, B, S = oracle.q8_bound(qb, xb)
+    _, mb = oracle.q8_quantize_blocks(xb)
+    assert mb[0, 1] == 0.0 and abs(S[0, 0] - A[0, 0]) <= B[0, 0]
+    assert abs(S[0, 0] - A[0, 0]) > 0.5 * B[0, 0] > 0
