@@ -128,7 +128,7 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
 
     alt_ms = None
     if alt() is not None:
-        for _ in range(max(2, warmup // 4)):
+        for _ in range(warmup):  # the same warm-up as the timed path
             alt()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
