@@ -99,6 +99,8 @@ struct MfmaFor<32, kAppendQ8> {
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
 __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a) {
   static_assert(MODE != kAppendQ8 || MS == 32, "int8 pre-filter uses the 32x32 MFMA");
+  static_assert(MODE != kAppendQ8 || (MS * RB <= 64 && 64 % (MS * RB) == 0),
+                "int8 pre-filter: a wave's rows of a tile must lie in one 64-row block (one meta entry)");
   typedef typename MfmaFor<MS, MODE>::type M;
   typedef typename M::acc_t acc_t;
   constexpr int RS = QS >= 4 ? 1 : 4 / QS;  // row splits
