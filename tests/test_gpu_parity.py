@@ -616,3 +616,40 @@ def test_index_auto_int8_at_size_is_exact():
     vf, i_f = idx.search(q, 10, method="fused")
     assert torch.equal(i, i_f)
     assert oracle.check_exact(q.numpy(), x.numpy(), 10, v.cpu().numpy(), i.cpu().numpy()) >= 0.99
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nq,n,d,k", [(1, 1, 64, 1), (3, 70, 128, 5), (1000, 3000, 384, 20), (2, 5000, 768, 256),
+                                      (5, 129, 1536, 129)])
+def test_q8_edge_shapes(eng, nq, n, d, k):
+    """Tiny corpora (no pre-pass: every list overflows and is rescanned), a
+    partial last block, many query groups, k = 256 and k > rows per block."""
+    say(f"q8 edge nq={nq} n={n} d={d} k={k}")
+    x, q = make(n, d, nq, seed=nq + n)
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    v8, i8 = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64)
+    assert oracle.check_exact(q.numpy(), x.numpy(), k, v8, i8) >= 0.99
+    np.testing.assert_allclose(v8, v.cpu().numpy(), rtol=0, atol=2e-6)
+
+
+@pytest.mark.gpu
+def test_q8_zero_queries_and_rows(eng):
+    """All-zero queries (scale 0) and all-zero corpus blocks: every score is 0 and
+    ties order by id."""
+    say("q8 zeros")
+    x, q = make(3000, 384, 4, seed=9)
+    x[64:256] = 0
+    q[1] = 0
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, 10)
+    v, i, _ = eng.fused_topk(qd, xd, 10)
+    torch.cuda.synchronize()
+    assert torch.equal(i8.cpu(), i.cpu())
+    assert i8[1].cpu().tolist() == list(range(10)) and (v8[1] == 0).all()
