@@ -61,7 +61,7 @@ def bench_grid(sizes, dims, batches, ks, methods, seed=0, target_s=0.3, log=prin
     total_mem = torch.cuda.get_device_properties(0).total_memory
     for d in dims:
         for n in sizes:
-            need = 2 * n * d + 4 * max(batches) * n + (1 << 30)
+            need = 3 * n * d + 4 * max(batches) * n + (1 << 30)  # fp16 corpus + int8 companion + scores
             if need > total_mem:
                 rows.append({"n": n, "d": d, "skipped": "memory"})
                 continue
@@ -114,7 +114,7 @@ def main():
     ap.add_argument("--dims", default="384,768")
     ap.add_argument("--batches", default="1,32,256")
     ap.add_argument("--ks", default="10,100")
-    ap.add_argument("--methods", default="fused,twopass,torch")
+    ap.add_argument("--methods", default="auto,fused,int8,twopass,torch")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--target-s", type=float, default=0.3)
     ap.add_argument("--out", default="results/gpu.json")

@@ -15,7 +15,7 @@ import argparse
 import json
 from pathlib import Path
 
-METHOD_ORDER = ["fused", "twopass", "torch", "faiss_gpu_fp16", "faiss_gpu_fp32", "faiss_cpu", "numpy"]
+METHOD_ORDER = ["auto", "fused", "int8", "twopass", "torch", "faiss_gpu_fp16", "faiss_gpu_fp32", "faiss_cpu", "numpy"]
 
 
 def short_n(n: int) -> str:

@@ -28,11 +28,15 @@ _NORM_CHUNK = 1 << 18
 # int8 pre-filter (an int8 companion of the corpus scanned instead of the fp16
 # rows; exact results).  Built by default for corpora of at least Q8_MIN_ROWS
 # rows wider than Q8_MIN_WIDTH; "auto" uses it where it measured faster than the
-# fp16 scan: batch 1 (bandwidth-bound GEMV on half the bytes), and batches with
-# k <= Q8_MAX_K over at least Q8_BATCH_MIN_ROWS rows.
+# fp16 scan (MI355X latency grid, 100k-4M rows x 384/768, k 10/100, batch
+# 1/32/256): batch 1 (bandwidth-bound GEMV on half the bytes), and over at least
+# Q8_BATCH_MIN_ROWS rows batches of at most Q8_MAX_BATCH queries or with
+# k <= Q8_MAX_K.  (Large batches with large k stay on the fp16 path: the int8
+# bound lets through ~3x the candidates, each an fp16 row read.)
 Q8_MIN_ROWS = 1 << 18
 Q8_MIN_WIDTH = 256
 Q8_MAX_K = 16
+Q8_MAX_BATCH = 64
 Q8_BATCH_MIN_ROWS = 1 << 19
 
 METHODS = ("auto", "fused", "twopass", "torch", "int8")
@@ -45,7 +49,8 @@ def int8_builds(n: int, width: int) -> bool:
 
 def int8_auto(n: int, width: int, nq: int, k: int) -> bool:
     """Whether method="auto" runs the int8 path (default companion, k <= 256)."""
-    return int8_builds(n, width) and k <= MAX_FUSED_K and (nq == 1 or (k <= Q8_MAX_K and n >= Q8_BATCH_MIN_ROWS))
+    return int8_builds(n, width) and k <= MAX_FUSED_K and (
+        nq == 1 or (n >= Q8_BATCH_MIN_ROWS and (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH)))
 
 
 def q8_row_bytes(width: int) -> int:
@@ -169,9 +174,9 @@ class Index:
             "int8"    - gfx950 engine over the int8 companion: int8 scan/GEMV with a
                         rigorous error bound, exact fp16 rescoring of what passes
                         (same results as "fused", k <= 256)
-            "auto"    - int8 where it is faster (batch 1, or k <= 16 over >= 2^19
-                        rows), else fused, for k <= 256; exact fp32 scores + row
-                        top-k for k <= 1024; else torch
+            "auto"    - int8 where it is faster (batch 1; over >= 2^19 rows, batches of
+                        <= 64 queries or k <= 16), else fused, for k <= 256; exact
+                        fp32 scores + row top-k for k <= 1024; else torch
         """
         if method not in METHODS:
             raise ValueError(f"method must be one of {METHODS}")
@@ -211,9 +216,9 @@ class Index:
 
     def _int8_wins(self, nq: int, k: int) -> bool:
         """Whether "auto" sends a batch of nq queries with this k to the int8 path."""
-        if self._xq is None:
+        if self._xq is None or k > MAX_FUSED_K:
             return False
-        return nq == 1 or (k <= Q8_MAX_K and len(self) >= Q8_BATCH_MIN_ROWS)
+        return nq == 1 or (len(self) >= Q8_BATCH_MIN_ROWS and (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH))
 
     def _search_large_k(self, q: torch.Tensor, k: int):
         """Exact top-k for MAX_FUSED_K < k <= MAX_EXACT_K on the GPU: fp32 score

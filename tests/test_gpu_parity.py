@@ -611,7 +611,8 @@ def test_index_auto_int8_at_size_is_exact():
     say(f"index auto int8 n={n}")
     x, q = make(n, 384, 8, seed=5)
     idx = Index(x, metric="ip")
-    assert idx._xq is not None and idx._int8_wins(8, 10) and not idx._int8_wins(8, 100)
+    assert idx._xq is not None and idx._int8_wins(8, 10) and idx._int8_wins(8, 100)
+    assert idx._int8_wins(256, 16) and not idx._int8_wins(256, 100) and not idx._int8_wins(8, 300)
     v, i = idx.search(q, 10)
     vf, i_f = idx.search(q, 10, method="fused")
     assert torch.equal(i, i_f)
