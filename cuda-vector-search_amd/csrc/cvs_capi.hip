@@ -104,7 +104,9 @@ int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
 // fit in registers with it; 16x16x32 for bq = 16 and for rows wider than 768.
 // bq = 256 at d <= 384 runs 8 waves (32 queries each, two per SIMD), so that
 // one wave's candidate epilogue and barrier waits overlap the other's MFMAs
-// (measured 7% faster than 4 waves of 64 queries).
+// (measured 7% faster than 4 waves of 64 queries).  The auto plan uses it at
+// d = 384 only: narrower rows run the runtime-width kernel, which spills at 256
+// registers per wave and is ~2x slower than two groups of 128 queries.
 bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
   switch (bq) {
     case 16:
@@ -201,7 +203,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     }
   } else {
     if (!forced_bq) {
-      bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d > 384) ? 128 : 256;
+      bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d != 384) ? 128 : 256;
       ScanCfg tmp;
       while (!cfg_for(bq, d, &tmp)) bq >>= 1;
     }
@@ -523,7 +525,7 @@ int cvs_scores(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, v
   // Same query blocks and chunking as the fused plan: one workgroup per CU,
   // chunks a multiple of the 8 XCDs when several query groups share them.
   ScanCfg cfg;
-  int64_t bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d > 384) ? 128 : 256;
+  int64_t bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d != 384) ? 128 : 256;
   while (!cfg_for(bq, d, &cfg)) bq >>= 1;
   const int64_t groups = ceil_div(nq, bq);
   const int64_t ntiles = ceil_div(n, cfg.tile_rows());

@@ -366,10 +366,31 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
       for (int rb = 0; rb < RB; ++rb)
         f[kk][rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
   };
-  half8 ab[2][KPS][RB];  // stage s in ab[s & 1] (static within a tile), stage s+1 prefetched
+  // 8-wave full-width tiles (256 registers per wave) read the A fragments of
+  // one k-step LA k-steps ahead into a ring of SL = LA + 1 slots (slot g % SL
+  // holds k-step g) instead of a whole stage ahead: 24 instead of 64 VGPRs of
+  // fragments.  Without it the 8-wave kernels spill, and the scratch reloads in
+  // the tile loop wait on vmcnt(0), draining the stage pipeline (C2 scan 239 us
+  // vs 192 us).  It syncs once per stage (paired sync would refill a buffer
+  // still being read); 4-wave kernels keep the stage-ahead scheme (4% faster).
+  constexpr int KT = NCMAX * KPS;  // k-steps per tile
+  constexpr int LA = 2, SL = LA + 1;
+  constexpr bool KRING = FULLW && NW == 8 && (KT % SL == 0);
+  half8 ab[KRING ? 1 : 2][KPS][RB];  // stage s in ab[s & 1] (static within a tile), stage s+1 prefetched
+  half8 fr[KRING ? SL : 1][RB];
+  auto read_ks = [&](int buf_idx, int kk, half8 (&f)[RB]) {
+    const unsigned char* buf = smem + buf_idx * STAGE;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
+  };
   wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
   __builtin_amdgcn_s_barrier();           // ... and for every wave
-  read_stage(0, ab[0]);
+  if (KRING) {
+#pragma unroll
+    for (int g = 0; g < LA; ++g) read_ks(0, g, fr[g]);
+  } else {
+    read_stage(0, ab[0]);
+  }
   int cur_buf = 0;
 
   for (int64_t t = t_begin; t < t_end; ++t) {
@@ -381,9 +402,31 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
 #pragma unroll
         for (int e = 0; e < M::NE; ++e) acc[qb][rb][e] = 0.f;
 
+    if (KRING) {
+#pragma unroll
+      for (int c = 0; c < NCMAX; ++c) {
+        // per-stage sync: stage c+1 has landed for every wave, and every read
+        // of stage c-1's buffer is retired before issue_next() refills it
+        wait_vmcnt_lgkm0<(NBUF - 3) * LPW>();
+        __builtin_amdgcn_s_barrier();
+        issue_next();
+        const int nxt = (cur_buf + 1 == NBUF) ? 0 : cur_buf + 1;
+#pragma unroll
+        for (int kk = 0; kk < KPS; ++kk) {
+          const int g = c * KPS + kk;
+          if (kk + LA < KPS) read_ks(cur_buf, kk + LA, fr[(g + LA) % SL]);
+          else read_ks(nxt, kk + LA - KPS, fr[(g + LA) % SL]);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) acc[qb][rb] = M::run(fr[g % SL][rb], qf[qb][g], acc[qb][rb]);
+        }
+        cur_buf = nxt;
+      }
+    }
 #pragma unroll
     for (int c = 0; c < NCMAX; ++c) {
-      if (c < nc) {
+      if (!KRING && c < nc) {
         // Stage s is in ab[c & 1].  Per-stage sync: wait until stage s+1 has
         // landed for every wave; the barrier also retires all reads of stage
         // s-1's buffer, which issue_next() refills with stage s+NBUF-1.  Paired
@@ -411,7 +454,7 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
         cur_buf = nxt;
       }
     }
-    if (nc & 1) {  // the next tile's first stage sits in ab[1]
+    if (!KRING && (nc & 1)) {  // the next tile's first stage sits in ab[1]
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
