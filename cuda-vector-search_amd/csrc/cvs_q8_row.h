@@ -16,18 +16,23 @@ __device__ __forceinline__ signed char q8_quant(float v, float inv) {
   return (signed char)fminf(127.f, fmaxf(-127.f, r));
 }
 
-// Whole wave; `lane` = lane id.  dst holds dq >= d bytes (zero past d).
-__device__ __forceinline__ void q8_query_row(const _Float16* src, int d, int dq, signed char* dst, float4* meta,
-                                             int lane) {
-  constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;
-  float v[kQ8RowPer];
-  float m = 0.f;
+// The row's elements for this lane (lane + 64 i), zero past d.
+__device__ __forceinline__ void q8_load_row(const _Float16* src, int d, int lane, float (&v)[kQ8RowPer]) {
 #pragma unroll
   for (int i = 0; i < kQ8RowPer; ++i) {
     const int c = i * kWave + lane;
     v[i] = c < d ? (float)src[c] : 0.f;
-    m = fmaxf(m, fabsf(v[i]));
   }
+}
+
+// Whole wave, on the values q8_load_row loaded; `lane` = lane id.  dst holds
+// dq >= d bytes (zero past d).
+__device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int d, int dq, signed char* dst,
+                                                float4* meta, int lane) {
+  constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < kQ8RowPer; ++i) m = fmaxf(m, fabsf(v[i]));
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   const float s = m / 127.f;
@@ -56,6 +61,13 @@ __device__ __forceinline__ void q8_query_row(const _Float16* src, int d, int dq,
     mt.w = 0.f;
     *meta = mt;
   }
+}
+
+__device__ __forceinline__ void q8_query_row(const _Float16* src, int d, int dq, signed char* dst, float4* meta,
+                                             int lane) {
+  float v[kQ8RowPer];
+  q8_load_row(src, d, lane, v);
+  q8_quantize_row(v, d, dq, dst, meta, lane);
 }
 
 }  // namespace cvs

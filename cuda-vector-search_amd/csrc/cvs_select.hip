@@ -176,8 +176,11 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int k = a.k;
   const int l16 = tid & 15;
   const int nd = RESCORE ? a.d / 8 : 0;  // 16-byte pieces per row
-  if (MODE == kSelTau && a.qq_out != nullptr && tid < kWave)  // int8 pre-filter: this query's int8 row
-    q8_query_row(a.q + (int64_t)q * a.d, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid);
+  // int8 pre-filter: wave 1 loads this query's row now and quantises it after
+  // the selection (the load latency hides behind the selection's work)
+  float qrow[kQ8RowPer];  // (dead outside the threshold mode)
+  const bool quant = MODE == kSelTau && a.qq_out != nullptr && tid >= kWave && tid < 2 * kWave;
+  if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
   half8 qv[RESCORE ? RL : 1];
   if (RESCORE) {
     const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
@@ -324,6 +327,8 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
 
   const int nb = min(S.nbuf, k);
+  if (MODE == kSelTau && quant)
+    q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
   if (MODE == kSelTau) {
     // the k-th best key is the smallest survivor
     if (tid < kWave) {
