@@ -1029,10 +1029,8 @@ int cvs_q8_build(const void* x, int64_t n, int64_t d, void* xq, int64_t xq_bytes
   if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
   Q8BuildArgs a{static_cast<const _Float16*>(x), n, (int)d, (int)L.dq, static_cast<signed char*>(xq),
                 reinterpret_cast<float4*>(static_cast<char*>(xq) + L.off_meta),
-                reinterpret_cast<unsigned*>(static_cast<char*>(xq) + L.off_xmax)};
-  hipError_t e = hipMemsetAsync(a.xmax, 0, 16, reinterpret_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
-  e = launch_q8_build(a, reinterpret_cast<hipStream_t>(stream));
+                reinterpret_cast<float*>(static_cast<char*>(xq) + L.off_xmax)};
+  hipError_t e = launch_q8_build(a, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "int8 corpus build launch");
   return CVS_OK;
 }

@@ -146,7 +146,7 @@ struct Q8BuildArgs {
   int dq;              // int8 row bytes (>= d, multiple of 128); columns d..dq are zero
   signed char* xq;     // [ceil(n/64)*64, dq]
   float4* bmeta;       // [ceil(n/64)]
-  unsigned* xmax;      // max over blocks of max|x_r|_2 (float bits; zeroed before the launch)
+  float* xmax;         // max over blocks of max|x_r|_2
 };
 
 // int8 queries: per-query scale and residual norms.

@@ -104,8 +104,19 @@ __global__ __launch_bounds__(kBlock) void q8_build_kernel(Q8BuildArgs a) {
     meta.z = fmaxf(fmaxf(xmax_s[0], xmax_s[1]), fmaxf(xmax_s[2], xmax_s[3]));
     meta.w = 0.f;
     a.bmeta[blk] = meta;
-    atomicMax(a.xmax, __float_as_uint(meta.z));  // non-negative floats order as their bits
   }
+}
+
+// One workgroup: the corpus-wide maximum row norm (max of the blocks' .z).
+__global__ __launch_bounds__(kBlock) void q8_xmax_kernel(const float4* bmeta, int64_t nblk, float* xmax) {
+  __shared__ float red[kBlock / kWave];
+  float m = 0.f;
+  for (int64_t b = threadIdx.x; b < nblk; b += kBlock) m = fmaxf(m, bmeta[b].z);
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) *xmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 // One wave per query row.
@@ -122,6 +133,7 @@ hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
   const int64_t blocks = (a.n + 63) / 64;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(q8_build_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL(q8_xmax_kernel, dim3(1), dim3(kBlock), 0, s, a.bmeta, blocks, a.xmax);
   return hipGetLastError();
 }
 
