@@ -59,20 +59,36 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // compiler's own LDS-DMA tracking cannot tell the stage buffers apart and
 // would insert a full vmcnt(0) wait before every LDS read, serialising the
 // pipeline.  Callers therefore own all waits (wait_vmcnt* + s_barrier) before
-// reading a block.  `lds_base` must be wave-uniform.
+// reading a block.  `lds_base` must be wave-uniform.  NT marks the load
+// non-temporal, for data streamed once per launch (the int8 corpus companion:
+// keeping it out of the caches' retained lines leaves them to the fp16 rows
+// that rescoring re-reads; 4-12 us less rescoring at 1M rows).  It is slower
+// for fp16 scans, whose query groups share corpus lines through L2.  Callers
+// load whole 128-byte lines.
+template <bool NT>
 __device__ __forceinline__ void dma_to_lds_16(const void* src, const void* lds_block) {
   const uint32_t base = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_block);
   // m0 is restored afterwards: the compiler treats it as reserved.
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(base), "v"(src)
-      : "memory");
+  if (NT)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(src)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(src)
+        : "memory");
 }
 
 // ---- register placement -----------------------------------------------------

@@ -161,10 +161,15 @@ struct Q8QueryArgs {
 
 // Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,
 // tile rows = rs*rb*ms, widest row = ksmax * (ms == 16 ? 32 : 16).
+// Row splits of a scan configuration (waves = qs * rs): 4 waves, one per SIMD,
+// except 8 (two per SIMD) for qs = 8.
+constexpr int scan_row_splits(int qs) { return qs >= 4 ? 1 : 4 / qs; }
+constexpr int scan_waves(int qs) { return qs * scan_row_splits(qs); }
+
 struct ScanCfg {
   int ms, qs, qb, rb, ksmax;
   int bq() const { return qs * ms * qb; }
-  int rs() const { return qs >= 4 ? 1 : 4 / qs; }  // row splits (waves = qs * rs)
+  int rs() const { return scan_row_splits(qs); }
   int tile_rows() const { return rs() * rb * ms; }
   int wave_rows() const { return rb * ms; }
   int dmax() const { return ksmax * (ms == 16 ? 32 : 16); }

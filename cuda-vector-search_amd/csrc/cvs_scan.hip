@@ -14,10 +14,10 @@
 //    throughput of v_mfma_f32_16x16x32_f16, which is kept (MS = 16) for batch
 //    <= 16 and for rows wider than 768.
 //  * Corpus rows stream HBM -> LDS with global_load_lds_dwordx4 (no VGPR
-//    staging), in 64-column stages.  Each 1 KB block of a stage is exactly one
-//    MFMA A fragment in lane order, so the ds_read_b128 that feeds the MFMA is
-//    contiguous and conflict free.  NBUF stages are in flight (40-56 KB per
-//    CU); waits are explicit vmcnt counts.
+//    staging), in 64-column (128-byte) stages, each load reading 8 whole
+//    128-byte lines; the rows' 16-byte pieces are permuted in LDS so that the
+//    ds_read_b128s feeding the MFMAs are free of bank conflicts.  NBUF stages
+//    are in flight (40-56 KB per CU); waits are explicit vmcnt counts.
 //  * Scores never leave VGPRs.  kAppend filters them against a per-query
 //    threshold (from the sampling pre-pass): a lane whose block maximum passes
 //    copies its whole row of scores to an LDS staging area (a few ds_writes,
@@ -34,6 +34,8 @@
 //             receives D[4(l/16)+i][l%16], i = 0..3.
 //   32x32x16: lane l supplies A[l%32][8(l/32)..+7], B[8(l/32)..+7][l%32] and
 //             receives D[8i+4(l/32)+j][l%32], i, j = 0..3 (element 4i+j).
+#include <climits>
+
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 
@@ -96,14 +98,21 @@ struct MfmaFor<32, kAppendQ8> {
 // FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
 // compile-time constant (per-stage guards on a runtime count split the
 // unrolled stage loop into separate blocks and cost ~15% of the scan).
+// Stage buffers hold TR rows x 128 bytes (64 halfs), row-major.  A DMA load
+// fills 1 KB = 8 rows: lane l fetches a 16-byte piece of row l/8 into slot l%8,
+// so every load reads 8 whole 128-byte lines.  Slot s of row R holds piece
+// s ^ piece_swz(R): the 8 (and 16) consecutive rows whose equal-index pieces
+// the lanes of one fragment read then fall on distinct LDS banks.
+__device__ __forceinline__ int piece_swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
-__global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a) {
+__global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArgs a) {
   static_assert(MODE != kAppendQ8 || MS == 32, "int8 pre-filter uses the 32x32 MFMA");
   static_assert(MODE != kAppendQ8 || (MS * RB <= 64 && 64 % (MS * RB) == 0),
                 "int8 pre-filter: a wave's rows of a tile must lie in one 64-row block (one meta entry)");
   typedef typename MfmaFor<MS, MODE>::type M;
   typedef typename M::acc_t acc_t;
-  constexpr int RS = QS >= 4 ? 1 : 4 / QS;  // row splits
+  constexpr int RS = scan_row_splits(QS);  // row splits
   constexpr int NW = QS * RS;       // waves: 4 (one per SIMD) or 8 (two per SIMD)
   constexpr int NT = NW * kWave;
   constexpr int QW = MS * QB;        // queries per wave
@@ -114,6 +123,7 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
   constexpr int FPS = TRB * KPS;     // A fragments (1 KB each) per stage
   static_assert(FPS % NW == 0, "every wave must issue the same number of stage loads");
+  static_assert(FPS * 8 == TR, "a stage load covers 8 rows of 128 bytes");
   constexpr int LPW = FPS / NW;      // stage loads per wave
   constexpr int STAGE = FPS * 1024;
   constexpr int NBUF = ((QS >= 4 ? 56 : 40) * 1024) / STAGE + 2;
@@ -195,11 +205,14 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   // of its first 64-column stage), advanced incrementally.
   const _Float16* src[LPW];
   int64_t src_row[LPW];
+  int poff[LPW];  // this lane's 16-byte piece of its row, in halfs
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int f = w + NW * j;
-    src_row[j] = t_begin * TR + (f % TRB) * MS + col;
-    src[j] = a.x + src_row[j] * d + (f / TRB) * M::KSZ + kg * 8;
+    const int rl = f * 8 + (lane >> 3);  // tile row of this lane's load
+    poff[j] = ((lane & 7) ^ piece_swz(rl)) * 8;
+    src_row[j] = t_begin * TR + rl;
+    src[j] = a.x + src_row[j] * d + poff[j];
   }
   auto issue_next = [&]() {
     unsigned char* buf = smem + it_buf * STAGE;
@@ -208,8 +221,8 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
     for (int j = 0; j < LPW; ++j) {
       const int f = w + NW * j;
       const _Float16* p = src[j] + it_c * 64;
-      if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * 64 + (f / TRB) * M::KSZ + kg * 8;
-      dma_to_lds_16(p, buf + f * 1024);
+      if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * 64 + poff[j];
+      dma_to_lds_16<Q8>(p, buf + f * 1024);
     }
     if (++it_c == nc) {
       it_c = 0;
@@ -358,13 +371,20 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
 
   // A fragments of one stage (KPS k-steps x RB row blocks), read from LDS one
   // stage ahead of the MFMAs that consume them.
+  // A fragment of k-step kk, row block rb: row R = (rs*RB + rb)*MS + col, piece
+  // kk*G + kg, at R*128 + ((piece ^ piece_swz(R)) << 4); piece_swz(R) depends on
+  // R mod 16 = col mod 16 only, so one lane offset per k-step serves every rb.
+  int aoff[KPS];
+#pragma unroll
+  for (int kk = 0; kk < KPS; ++kk)
+    aoff[kk] = (rs * RB * MS + col) * 128 + (((kk * G + kg) ^ piece_swz(col)) << 4);
   auto read_stage = [&](int buf_idx, half8 (&f)[KPS][RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
     for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
-        f[kk][rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
+        f[kk][rb] = *(const half8*)(buf + aoff[kk] + rb * MS * 128);
   };
   // 8-wave full-width tiles (256 registers per wave) read the A fragments of
   // one k-step LA k-steps ahead into a ring of SL = LA + 1 slots (slot g % SL
@@ -381,7 +401,7 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
   auto read_ks = [&](int buf_idx, int kk, half8 (&f)[RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + (kk * TRB + rs * RB + rb) * 1024 + lane * 16);
+    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + aoff[kk] + rb * MS * 128);
   };
   wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
   __builtin_amdgcn_s_barrier();           // ... and for every wave
@@ -487,46 +507,79 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
       bm = float4{m[0], m[1], m[2], m[3]};
     }
     const bool partial = (t * TR + TR > n);
+    // kAppend / kAppendQ8: stage row block rb of query block qb (block maximum
+    // m) for every lane whose maximum passes; val(e) is the lane's score e.
+    auto stage = [&](int qb, int rb, float m, auto val) {
+      uint64_t mk = __ballot(m >= thr[qb]);
+      if (mk) {
+        if (st_n + __popcll(mk) > STCAP) {
+          flush();
+          mk = __ballot(m >= thr[qb]);
+        }
+        if (m >= thr[qb]) {
+          const int p = st_n + lanes_below(mk);
+#pragma unroll
+          for (int c = 0; c < M::NE / 4; ++c)
+            *(f32x4*)(&st_val[w][p * EST + 4 * c]) = f32x4{val(4 * c), val(4 * c + 1), val(4 * c + 2), val(4 * c + 3)};
+          st_meta[w][2 * p] = qs * QW + qb * MS + col;
+          st_meta[w][2 * p + 1] = (int)rowb + rb * MS;
+        }
+        st_n += __popcll(mk);
+      }
+    };
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
-      float v[NV];
-      if (Q8) {  // upper bound of each exact score: A + slack
+      if constexpr (Q8) {
+        // Upper bound of each exact score: A + slack with A = cq * acc and
+        // cq >= 0, so the largest bound of a row block is that of its largest
+        // int32 sum (conversion and fma round monotonically): the filter needs
+        // one conversion per block, the rest only for staged blocks.
         const float cq = qm[qb].x * bm.x;
         const float slack = (fmaf(qm[qb].y, bm.y, qm[qb].z * bm.z) +
                              a.gamma * (qm[qb].y + qm[qb].z) * (bm.y + bm.z)) * (1.0f + 1.0f / 1048576.0f);
+        if (partial) {  // only the corpus's last tile has rows past n: not in the block maximum
+          const int64_t left = n - rowb;
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+          for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = fmaf((float)acc[qb][rb][e], cq, slack);
+            for (int e = 0; e < M::NE; ++e)
+              if (rb * MS + M::row(e) >= left) acc[qb][rb][e] = INT_MIN;
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          int mi = acc[qb][rb][0];
+#pragma unroll
+          for (int e = 1; e < M::NE; ++e) mi = max(mi, acc[qb][rb][e]);
+          stage(qb, rb, fmaf((float)mi, cq, slack), [&](int e) { return fmaf((float)acc[qb][rb][e], cq, slack); });
+        }
       } else {
+        float v[NV];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
           for (int e = 0; e < M::NE; ++e) v[rb * M::NE + e] = acc[qb][rb][e];
-      }
-      if (partial) {  // only the corpus's last tile has rows past n
-        const int64_t left = n - rowb;
+        if (partial) {  // only the corpus's last tile has rows past n
+          const int64_t left = n - rowb;
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+          for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int e = 0; e < M::NE; ++e)
-            if (rb * MS + M::row(e) >= left) v[rb * M::NE + e] = -__builtin_inff();
-      }
-
-      if (STORE) {  // into this wave's LDS tile: [query qb*MS + col][row rb*MS + 4kg + row(e)]
-        const int qo = (qb * MS + col) * SROW + 4 * kg;
-#pragma unroll
-        for (int j = 0; j < NV; j += 4) {  // elements 4c..4c+3 are 4 consecutive rows
-          const int r = (j / M::NE) * MS + M::row(j % M::NE);
-          if (MODE == kStoreF32)
-            *(f32x4*)(&stg[w][qo + r]) = f32x4{v[j], v[j + 1], v[j + 2], v[j + 3]};
-          else
-            *(half4*)((_Float16*)stg[w] + qo + r) =
-                half4{(_Float16)v[j], (_Float16)v[j + 1], (_Float16)v[j + 2], (_Float16)v[j + 3]};
+            for (int e = 0; e < M::NE; ++e)
+              if (rb * MS + M::row(e) >= left) v[rb * M::NE + e] = -__builtin_inff();
         }
-      } else {
-        if (MODE == kMax) {
+
+        if (STORE) {  // into this wave's LDS tile: [query qb*MS + col][row rb*MS + 4kg + row(e)]
+          const int qo = (qb * MS + col) * SROW + 4 * kg;
+#pragma unroll
+          for (int j = 0; j < NV; j += 4) {  // elements 4c..4c+3 are 4 consecutive rows
+            const int r = (j / M::NE) * MS + M::row(j % M::NE);
+            if (MODE == kStoreF32)
+              *(f32x4*)(&stg[w][qo + r]) = f32x4{v[j], v[j + 1], v[j + 2], v[j + 3]};
+            else
+              *(half4*)((_Float16*)stg[w] + qo + r) =
+                  half4{(_Float16)v[j], (_Float16)v[j + 1], (_Float16)v[j + 2], (_Float16)v[j + 3]};
+          }
+        } else if (MODE == kMax) {
           float m = v[0];
 #pragma unroll
           for (int j = 1; j < NV; ++j) m = fmaxf(m, v[j]);
@@ -540,24 +593,7 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
             float m = v[rb * M::NE];
 #pragma unroll
             for (int e = 1; e < M::NE; ++e) m = fmaxf(m, v[rb * M::NE + e]);
-            uint64_t mk = __ballot(m >= thr[qb]);
-            if (mk) {
-              if (st_n + __popcll(mk) > STCAP) {
-                flush();
-                mk = __ballot(m >= thr[qb]);
-              }
-              if (m >= thr[qb]) {
-                const int p = st_n + lanes_below(mk);
-#pragma unroll
-                for (int c = 0; c < M::NE / 4; ++c)
-                  *(f32x4*)(&st_val[w][p * EST + 4 * c]) =
-                      f32x4{v[rb * M::NE + 4 * c], v[rb * M::NE + 4 * c + 1], v[rb * M::NE + 4 * c + 2],
-                            v[rb * M::NE + 4 * c + 3]};
-                st_meta[w][2 * p] = qs * QW + qb * MS + col;
-                st_meta[w][2 * p + 1] = (int)rowb + rb * MS;
-              }
-              st_n += __popcll(mk);
-            }
+            stage(qb, rb, m, [&](int e) { return v[rb * M::NE + e]; });
           }
         }
       }
@@ -629,7 +665,7 @@ __global__ __launch_bounds__(QS == 8 ? 512 : 256, 1) void scan_kernel(ScanArgs a
 template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one_q8(const ScanArgs& a, int grid, hipStream_t s) {
   if (a.d != KS * MfmaI8::KSZ || a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendQ8, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+  hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendQ8, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
   return hipGetLastError();
 }
 
@@ -639,27 +675,27 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   switch (mode) {
     case kAppend:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       break;
     case kMax:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       break;
     case kStoreF32:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       break;
     case kStoreF16:
       if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, true>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(QS == 8 ? 512 : 256), 0, s, a);
+        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;
