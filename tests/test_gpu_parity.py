@@ -496,7 +496,9 @@ def test_q8_build_matches_oracle(eng, n, d):
 
 
 Q8_CASES = [(1, 30000, 384, 10), (7, 20000, 320, 5), (33, 25000, 384, 64), (65, 30000, 512, 10),
-            (129, 20000, 768, 100), (256, 40000, 384, 10), (300, 20000, 1024, 256), (40, 20000, 1536, 1)]
+            (129, 20000, 768, 100), (256, 40000, 384, 10), (300, 20000, 1024, 256), (40, 20000, 1536, 1),
+            # 8-wave int8 kernels with a sampled threshold and a partial last tile
+            (256, 300001, 384, 10), (200, 262193, 768, 16)]
 
 
 @pytest.mark.gpu
