@@ -758,24 +758,24 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   }
   if (!scan_cfg_available(P.cfg, kAppendQ8)) return fail(CVS_ERR_INVALID, "internal: no int8 scan for width %lld", (long long)d);
   if (!P.gemv) {
-  P.bq = P.cfg.bq();
-  P.groups = ceil_div(std::max<int64_t>(nq, 1), P.bq);
-  P.ntiles = ceil_div(n, P.cfg.tile_rows());
-  const int64_t rs = P.cfg.rs();
-  const int64_t max_chunks = std::min<int64_t>({P.ntiles, 65535, kSelectMaxLists / rs});
-  int64_t c = std::max<int64_t>(1, ceil_div(cus, P.groups));
-  c = std::min<int64_t>(c, std::max<int64_t>(1, P.ntiles / 2));
-  c = std::min<int64_t>(c, max_chunks);
-  if (P.groups > 1 && c >= 8) {
-    c = std::min<int64_t>(align_up(c, 8), (max_chunks / 8) * 8);
-    P.tpc = ceil_div(P.ntiles, c);
-  } else {
-    P.tpc = ceil_div(P.ntiles, c);
-    c = ceil_div(P.ntiles, P.tpc);
-  }
-  P.chunks = c;
-  P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
-  P.nlists = c * rs;
+    P.bq = P.cfg.bq();
+    P.groups = ceil_div(std::max<int64_t>(nq, 1), P.bq);
+    P.ntiles = ceil_div(n, P.cfg.tile_rows());
+    const int64_t rs = P.cfg.rs();
+    const int64_t max_chunks = std::min<int64_t>({P.ntiles, 65535, kSelectMaxLists / rs});
+    int64_t c = std::max<int64_t>(1, ceil_div(cus, P.groups));
+    c = std::min<int64_t>(c, std::max<int64_t>(1, P.ntiles / 2));
+    c = std::min<int64_t>(c, max_chunks);
+    if (P.groups > 1 && c >= 8) {
+      c = std::min<int64_t>(align_up(c, 8), (max_chunks / 8) * 8);
+      P.tpc = ceil_div(P.ntiles, c);
+    } else {
+      P.tpc = ceil_div(P.ntiles, c);
+      c = ceil_div(P.ntiles, P.tpc);
+    }
+    P.chunks = c;
+    P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
+    P.nlists = c * rs;
   }
   P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
   if (P.groups * P.chunks > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
@@ -933,29 +933,29 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     e = launch_gemv(1536, g, (int)P.gemv_grid, s);
     if (e != hipSuccess) return hip_fail(e, "int8 gemv launch");
   } else {
-  ScanArgs a{};
-  a.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
-  a.x = static_cast<const _Float16*>(xq);
-  a.n = n;
-  a.nq = (int)nq;
-  a.d = (int)(P.dq / 2);
-  a.groups = (int)P.groups;
-  a.nchunks = (int)P.chunks;
-  a.ntiles = P.ntiles;
-  a.tpc = P.tpc;
-  a.xcd_pair = P.xcd_pair;
-  a.tau = S.prepass ? tau : nullptr;
-  a.lv = lv;
-  a.li = li;
-  a.lcount = cnt;
-  a.nlists = (int)P.nlists;
-  a.cap = (int)P.cap;
-  a.k = (int)k;
-  a.qmeta = qm;
-  a.bmeta = bmeta;
-  a.gamma = gamma;
-  e = launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
-  if (e != hipSuccess) return hip_fail(e, "int8 scan launch");
+    ScanArgs a{};
+    a.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
+    a.x = static_cast<const _Float16*>(xq);
+    a.n = n;
+    a.nq = (int)nq;
+    a.d = (int)(P.dq / 2);
+    a.groups = (int)P.groups;
+    a.nchunks = (int)P.chunks;
+    a.ntiles = P.ntiles;
+    a.tpc = P.tpc;
+    a.xcd_pair = P.xcd_pair;
+    a.tau = S.prepass ? tau : nullptr;
+    a.lv = lv;
+    a.li = li;
+    a.lcount = cnt;
+    a.nlists = (int)P.nlists;
+    a.cap = (int)P.cap;
+    a.k = (int)k;
+    a.qmeta = qm;
+    a.bmeta = bmeta;
+    a.gamma = gamma;
+    e = launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
+    if (e != hipSuccess) return hip_fail(e, "int8 scan launch");
   }
   mark(3);
   SelectArgs fa{};

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int TR = RS * RW;        // tile rows
   constexpr int KPS = 64 / M::KSZ;   // MFMA k-steps per 64-column stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
-  constexpr int FPS = TRB * KPS;     // A fragments (1 KB each) per stage
+  constexpr int FPS = TRB * KPS;     // 1 KB DMA loads (8 rows x 128 bytes) per stage
   static_assert(FPS % NW == 0, "every wave must issue the same number of stage loads");
   static_assert(FPS * 8 == TR, "a stage load covers 8 rows of 128 bytes");
   constexpr int LPW = FPS / NW;      // stage loads per wave
