@@ -166,9 +166,10 @@ COPY_KERNEL = re.compile(r"copyBuffer")  # torch copy_ between device tensors = 
 COPY_BYTES = 1 << 30
 
 
-def pmc_child(name):
-    """Body of one ``rocprofv3 --pmc`` child: a few searches of config `name`,
-    then a plain device copy of COPY_BYTES for the counter's calibration."""
+def pmc_child(name, method="auto"):
+    """Body of one ``rocprofv3 --pmc`` child: a few searches of config `name`
+    (Index.search with `method`), then a plain device copy of COPY_BYTES for the
+    counter's calibration."""
     import torch
 
     from cuda_vector_search import Index, synthetic
@@ -180,7 +181,7 @@ def pmc_child(name):
     q = synthetic.unit_queries(b, d, seed=1, device="cuda")
     index = Index(x, metric="ip", copy=False)
     for _ in range(3):
-        index.search(q, k)
+        index.search(q, k, method=method)
     torch.cuda.synchronize()
     del index, x
     src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device="cuda")
@@ -189,7 +190,7 @@ def pmc_child(name):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"pmc child {name}: 3 searches, 3 copies of {COPY_BYTES} bytes", flush=True)
+    print(f"pmc child {name}: 3 searches (method {method}), 3 copies of {COPY_BYTES} bytes", flush=True)
 
 
 def dominant_key(name):
@@ -311,9 +312,10 @@ def main():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     ap.add_argument("--pmc-child", metavar="CONFIG", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-method", default="auto", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
-        pmc_child(args.pmc_child)
+        pmc_child(args.pmc_child, args.pmc_method)
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
