@@ -656,3 +656,74 @@ def test_q8_zero_queries_and_rows(eng):
     torch.cuda.synchronize()
     assert torch.equal(i8.cpu(), i.cpu())
     assert i8[1].cpu().tolist() == list(range(10)) and (v8[1] == 0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["fused", "int8", "gemv"])
+def test_graph_capture_replays_match_eager(eng, path):
+    """The search issues no memset, allocation or synchronisation, so a HIP graph
+    captures it: every replay (with eager searches and syncs in between) returns
+    exactly the eager result."""
+    say(f"graph capture {path}")
+    nq = 1 if path == "gemv" else 64
+    x, q = make(40000, 384, nq, seed=17)
+    qd = q.cuda().contiguous()
+    xd = x.cuda().contiguous()
+    xq = eng.q8_build(xd) if path == "int8" else None
+    fn = (lambda: eng.q8_topk(qd, xd, xq, 10)) if path == "int8" else (lambda: eng.fused_topk(qd, xd, 10))
+    ref = fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], ref[0]) and torch.equal(out[1], ref[1])
+        again = fn()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(again[1], ref[1])
+
+
+@pytest.mark.gpu
+def test_concurrent_searches_on_threads_and_streams(eng):
+    """Re-entrant entry points: four threads, each on its own stream, search
+    different query batches at once; results equal the sequential ones."""
+    import threading
+
+    say("concurrent streams")
+    x, _ = make(30000, 384, 1, seed=23)
+    xd = x.cuda().contiguous()
+    xq = eng.q8_build(xd)
+    batches = [make(1, 384, nq, seed=100 + t)[1].cuda().contiguous() for t, nq in enumerate((1, 40, 130, 256))]
+    expect = [(eng.q8_topk(b, xd, xq, 16)[1].cpu(), eng.fused_topk(b, xd, 16)[1].cpu()) for b in batches]
+    torch.cuda.synchronize()
+    results, errors = [None] * len(batches), []
+
+    def work(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                got = []
+                for _ in range(5):
+                    got.append((eng.q8_topk(batches[t], xd, xq, 16)[1], eng.fused_topk(batches[t], xd, 16)[1]))
+                s.synchronize()
+            results[t] = [(a.cpu(), b.cpu()) for a, b in got]
+        except Exception as exc:  # reported below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(len(batches))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for t, res in enumerate(results):
+        for a, b in res:
+            assert torch.equal(a, expect[t][0]) and torch.equal(b, expect[t][1])
