@@ -699,6 +699,14 @@ namespace {
 
 constexpr int64_t kQ8SampleDiv = 8;
 
+// From this batch size on, the select rescores the candidates itself (one
+// workgroup per query, the k of largest bound first, then only those that can
+// still enter); below it, a rescoring kernel over (query, list group) pairs
+// keeps more CUs busy.  Wider rows cost more per rescored candidate, so the
+// select's savings win earlier there (measured at 1M rows: from batch 128 at
+// d = 768, batch 160-192 at d = 384).
+int64_t q8_two_phase_batch(int64_t d) { return d > 384 ? 128 : 160; }
+
 // int8 row bytes for a row of d fp16 elements: one of the widths the int8
 // scan is instantiated for.
 int64_t q8_row_bytes(int64_t d) { return d <= 384 ? 384 : d <= 768 ? 768 : 1536; }
@@ -983,15 +991,19 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     fa.wave_rows = P.cfg.wave_rows();
     fa.rsplits = P.cfg.rs();
   }
-  // rescoring: about 4 workgroups per CU over (query, group of lists)
-  fa.tau_in = S.prepass ? tau : nullptr;
-  fa.qmeta = qm;
-  fa.xmax = reinterpret_cast<const float*>(static_cast<const char*>(xq) + L.off_xmax);
-  fa.gamma = (float)d / 16777216.0f;
-  fa.lpb = 256;
-  while (fa.lpb > 8 && nq * ceil_div(P.nlists, fa.lpb) < 4 * (int64_t)di.cus) fa.lpb /= 2;
-  e = launch_rescore(fa, (int)nq, s);
-  if (e != hipSuccess) return hip_fail(e, "rescore launch");
+  if (nq < q8_two_phase_batch(d)) {
+    // rescoring spread over about 4 workgroups per CU, (query, group of lists)
+    // each; the select then sees exact scores
+    fa.exact = 1;
+    fa.tau_in = S.prepass ? tau : nullptr;
+    fa.qmeta = qm;
+    fa.xmax = reinterpret_cast<const float*>(static_cast<const char*>(xq) + L.off_xmax);
+    fa.gamma = (float)d / 16777216.0f;
+    fa.lpb = 256;
+    while (fa.lpb > 8 && nq * ceil_div(P.nlists, fa.lpb) < 4 * (int64_t)di.cus) fa.lpb /= 2;
+    e = launch_rescore(fa, (int)nq, s);
+    if (e != hipSuccess) return hip_fail(e, "rescore launch");
+  }
   e = launch_select(2, fa, (int)nq, s);
   if (e != hipSuccess) return hip_fail(e, "rescore select launch");
   mark(4);

@@ -115,8 +115,8 @@ struct SelectArgs {
   void* out_i;         // [nq, k] int32, or int64 when ids64 (final mode)
   int ids64;
   float* tau;          // [nq]    (threshold mode: score of the k-th best)
-  // rescore mode: candidates are row ids only; their exact fp16 scores are
-  // recomputed here.  A list whose count exceeds cap overflowed in the scan and
+  // rescore mode: lv holds each candidate's score upper bound; exact fp16
+  // scores are recomputed here.  A list whose count exceeds cap overflowed in the scan and
   // stands for every row of its range, all of which are rescored.
   const _Float16* q;   // [nq, d]
   const _Float16* x;   // [n, d]
@@ -124,6 +124,7 @@ struct SelectArgs {
   int d;
   int64_t ntiles, tpc; // the scan's tiles and tiles per chunk
   int tile_rows, wave_rows, rsplits;  // list L = chunk * rsplits + r
+  int exact;           // 1: rescore_kernel has already replaced the bounds by exact scores
   int lpb;             // rescore kernel: lists per workgroup
   // rescore kernel: candidates whose exact score is below the sampled
   // threshold by more than the fp32 rounding slack are dropped
@@ -180,10 +181,10 @@ struct ScanCfg {
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
 hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
 hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);  // 0 final, 1 threshold, 2 rescore
+hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
 hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s);
 hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s);
-hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_q8_queries(const Q8QueryArgs& a, hipStream_t s);
 
 bool scan_cfg_available(const ScanCfg& cfg, int mode);

@@ -16,12 +16,13 @@
 // per query holding a whole score row it is also the row top-k of a score
 // matrix (k up to 1024: the large-k path).
 //
-// Rescore mode finishes the int8 pre-filter: list entries are row ids whose
-// score bound reached the threshold, and each one's exact score is recomputed
-// here from the fp16 rows (fp32 accumulation, v_dot2_f32_f16) before it enters
-// the selection.  A list that overflowed in the scan (count > cap) is replaced
-// by every row of its corpus range, so the result stays exact whatever the
-// data.
+// Rescore mode finishes the int8 pre-filter: list entries are (score upper
+// bound, row id) pairs whose bound reached the threshold, and exact scores are
+// recomputed here from the fp16 rows (fp32 accumulation, v_dot2_f32_f16), first
+// for the k candidates of largest bound and then only for the others whose
+// bound reaches the k-th best exact score found so far.  A list that
+// overflowed in the scan (count > cap) is replaced by every row of its corpus
+// range, so the result stays exact whatever the data.
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 #include "cvs_q8_row.h"
@@ -139,7 +140,38 @@ __device__ void block_sort_desc(uint64_t* keys, int N) {
   }
 }
 
-constexpr int kSelFinal = 0, kSelTau = 1, kSelRescore = 2, kSelRescoreWide = 3;
+// Descending sort of keys[0..nb) in place for nb <= kBlock: thread t counts the
+// keys above its own (keys are unique, so the counts are a permutation of
+// 0..nb-1) and moves its key to that slot.  Two barriers instead of the
+// bitonic network's log2(N)(log2(N)+1)/2; every lane reads the same key at a
+// time (an LDS broadcast).  Whole block.
+__device__ void block_rank_sort(uint64_t* keys, int nb) {
+  const int tid = threadIdx.x;
+  uint64_t mine = 0;
+  int rank = 0;
+  if (tid < nb) {
+    mine = keys[tid];
+    for (int i = 0; i < nb; ++i) rank += keys[i] > mine ? 1 : 0;
+  }
+  __syncthreads();
+  if (tid < nb) keys[rank] = mine;
+  __syncthreads();
+}
+
+// Descending sort of keys[0..nb) (nb <= kBuf / 2 when nb > kBlock).  Whole block.
+__device__ void block_sort_keys(uint64_t* keys, int nb) {
+  if (nb <= kBlock) {
+    block_rank_sort(keys, nb);
+    return;
+  }
+  int N = 2;
+  while (N < nb) N <<= 1;
+  for (int i = nb + threadIdx.x; i < N; i += kBlock) keys[i] = 0ull;
+  __syncthreads();
+  block_sort_desc(keys, N);
+}
+
+constexpr int kSelFinal = 0, kSelTau = 1, kSelRescore = 2, kSelRescoreWide = 3, kSelRescoreMid = 4;
 constexpr int kMaxD = 1536;
 
 // Entries of list L of query q: its count, or in rescore mode the size of its
@@ -151,52 +183,40 @@ __device__ __forceinline__ int list_len(const SelectArgs& a, int q, int L, bool 
   return c;
 }
 
-// Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
-// l, l+16, ... (RL of them at most); each group works on RU candidates at once,
-// so RL*RU independent loads per lane are in flight.  RL = 4 covers d <= 512,
-// RL = 12 (one candidate at a time) d <= 1536.  (RU = 4 measured 8 us faster
-// than 8 at C2: fewer registers, more waves in flight.)
-template <int MODE>
-struct RescoreShape {
-  static constexpr int RL = MODE == kSelRescoreWide ? 12 : 4;
-  static constexpr int RU = MODE == kSelRescoreWide ? 1 : 4;
-};
-
-template <int MODE>
-__global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
-  __shared__ SelShared S;
-  constexpr bool RESCORE = (MODE == kSelRescore || MODE == kSelRescoreWide);
-  constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
-  __shared__ int sids[RESCORE ? kBatch : 1];  // a batch's candidate row ids (-1: none)
-  __shared__ unsigned ovf[RESCORE ? kSelectMaxLists / 32 : 1];  // overflowed-list bitmap
-  __shared__ int batch_ovf;  // the current batch holds rows of overflowed lists
+// Exclusive prefix sums of query q's list lengths into S.pre[0..NL], and an
+// empty key buffer.  Each thread reads the counts of its (at most 32)
+// consecutive lists once.  In rescore mode a list whose count exceeds cap
+// overflowed in the scan and stands for its whole row range; its bit is set in
+// `ovf` (zeroed by the caller) and *any_ovf becomes 1.  Whole block; returns
+// the total (S.pre[NL]).
+template <class SH>
+__device__ int list_prefix(SH& S, const SelectArgs& a, int q, bool rescore, unsigned* ovf = nullptr,
+                           int* any_ovf = nullptr) {
+  constexpr int kPer = kSelectMaxLists / kBlock;
   const int tid = threadIdx.x;
-  const int q = blockIdx.x;
   const int NL = a.nlists;
-  const int k = a.k;
-  const int l16 = tid & 15;
-  const int nd = RESCORE ? a.d / 8 : 0;  // 16-byte pieces per row
-  // int8 pre-filter: wave 1 loads this query's row now and quantises it after
-  // the selection (the load latency hides behind the selection's work)
-  float qrow[kQ8RowPer];  // (dead outside the threshold mode)
-  const bool quant = MODE == kSelTau && a.qq_out != nullptr && tid >= kWave && tid < 2 * kWave;
-  if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
-  half8 qv[RESCORE ? RL : 1];
-  if (RESCORE) {
-    const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
-#pragma unroll
-    for (int m = 0; m < RL; ++m) {
-      const int c = l16 + 16 * m;
-      qv[m] = c < nd ? qr[c] : half8{};
-    }
-  }
-
-  // Exclusive prefix sum of the list counts.
   const int per = (NL + kBlock - 1) / kBlock;
   const int l0 = tid * per;
-  const int l1 = min(NL, l0 + per);
+  int len[kPer];
   int sum = 0;
-  for (int L = l0; L < l1; ++L) sum += list_len(a, q, L, RESCORE);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (j >= per) break;  // (uniform)
+    const int L = l0 + j;
+    int c = 0;
+    if (L < NL) {
+      c = a.lcount ? a.lcount[(int64_t)q * NL + L] : a.cap;
+      if (rescore && c > a.cap) {
+        c = (int)(a.tpc * a.wave_rows);
+        if (ovf) {
+          atomicOr(&ovf[L >> 5], 1u << (L & 31));
+          *any_ovf = 1;
+        }
+      }
+    }
+    len[j] = c;
+    sum += c;
+  }
   S.part[tid] = sum;
   if (tid == 0) {
     S.nbuf = 0;
@@ -225,111 +245,126 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
     if (tid == kWave - 1) S.pre[NL] = incl;
   }
   __syncthreads();
-  {
-    int run = S.part[tid];
-    for (int L = l0; L < l1; ++L) {
+  int run = S.part[tid];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (j >= per) break;
+    const int L = l0 + j;
+    if (L < NL) {
       S.pre[L] = run;
-      run += list_len(a, q, L, RESCORE);
+      run += len[j];
     }
-  }
-  if (RESCORE) {
-    for (int i = tid; i < (NL + 31) / 32; i += kBlock) ovf[i] = 0u;
-    __syncthreads();
-    for (int L = tid; L < NL; L += kBlock)
-      if (a.lcount[(int64_t)q * NL + L] > a.cap) atomicOr(&ovf[L >> 5], 1u << (L & 31));
   }
   __syncthreads();
-  const int total = S.pre[NL];
+  return S.pre[NL];
+}
 
+// The list holding flat entry gi: the largest L with S.pre[L] <= gi.
+template <class SH>
+__device__ __forceinline__ int list_of(const SH& S, int NL, int gi) {
+  int lo = 0, hi = NL;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (S.pre[mid] <= gi) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// End of a batch of appends: cuts the buffer to its k best keys (raising the
+// threshold key) when the next batch might not fit, or when this batch was the
+// last (a last buffer of at most kBlock keys is sorted instead, leaving its k
+// best first).  Whole block.  Every thread reads the count before any thread can
+// append again, so all take the same branch.
+template <class SH>
+__device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
+  __syncthreads();
+  const int nb = S.nbuf;
+  if (last && nb <= kBlock) {  // small: sort it outright and keep the first k
+    block_rank_sort(S.keys, nb);
+    if (threadIdx.x == 0 && nb > k) {
+      S.nbuf = k;
+      S.thr_key = S.keys[k - 1];
+    }
+  } else if (nb > kBuf - kBatch || (last && nb > k)) {
+    const uint64_t kth = block_keep_top(S, nb, k);
+    if (threadIdx.x == 0) {
+      S.nbuf = k;
+      S.thr_key = kth;
+    }
+  }
+  __syncthreads();
+}
+
+// Smallest of keys[0..nb) (~0 when nb == 0).  Whole block; `red` is kWaves
+// words of LDS.
+__device__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
+  const int tid = threadIdx.x;
+  uint64_t m = ~0ull;
+  for (int i = tid; i < nb; i += kBlock) m = min(m, keys[i]);
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
+  if (tid % kWave == 0) red[tid / kWave] = m;
+  __syncthreads();
+  uint64_t r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = min(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// Sorts the nb (<= k) surviving keys and writes row q of the outputs, padded
+// with (-inf, -1).  Whole block.
+__device__ void write_topk(SelShared& S, const SelectArgs& a, int q, int nb) {
+  const int tid = threadIdx.x;
+  const int k = a.k;
+  block_sort_keys(S.keys, nb);
+  for (int r = tid; r < k; r += kBlock) {
+    const bool ok = r < nb;
+    a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
+    const int id = ok ? key_id(S.keys[r]) : -1;
+    if (a.ids64)
+      ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
+    else
+      ((int*)a.out_i)[(int64_t)q * k + r] = id;
+  }
+}
+
+// Final and threshold modes: query blockIdx.x's candidate keys are streamed
+// through the LDS buffer in kBatch steps, each filtered against the running
+// k-th best key.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
+  __shared__ SelShared S;
+  const int tid = threadIdx.x;
+  const int q = blockIdx.x;
+  const int NL = a.nlists;
+  const int k = a.k;
+  // int8 pre-filter: wave 1 loads this query's row now and quantises it after
+  // the selection (the load latency hides behind the selection's work)
+  float qrow[kQ8RowPer];  // (dead outside the threshold mode)
+  const bool quant = MODE == kSelTau && a.qq_out != nullptr && tid >= kWave && tid < 2 * kWave;
+  if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
+
+  const int total = list_prefix(S, a, q, false);
   for (int base = 0; base < total; base += kBatch) {
     const uint64_t t = S.thr_key;
-    if (RESCORE) {
-      __syncthreads();  // (everyone has read batch_ovf of the previous batch)
-      if (tid == 0) batch_ovf = 0;
-      __syncthreads();
-    }
     for (int j = 0; j < kBatch / kBlock; ++j) {
       const int gi = base + j * kBlock + tid;
       if (gi < total) {
-        int lo = 0, hi = NL;  // largest L with pre[L] <= gi
-        while (hi - lo > 1) {
-          const int mid = (lo + hi) >> 1;
-          if (S.pre[mid] <= gi) lo = mid; else hi = mid;
-        }
-        const int idx = gi - S.pre[lo];
-        const int64_t off = ((int64_t)q * NL + lo) * a.cap + idx;
-        if (RESCORE) {
-          int id = -1;
-          if ((ovf[lo >> 5] >> (lo & 31)) & 1u) {  // overflowed: row idx of the list's range
-            const int64_t tile = (int64_t)(lo / a.rsplits) * a.tpc + idx / a.wave_rows;
-            const int64_t row = tile * a.tile_rows + (int64_t)(lo % a.rsplits) * a.wave_rows + idx % a.wave_rows;
-            id = (tile < a.ntiles && row < a.n) ? (int)row : -1;
-          } else {  // rescore_kernel has replaced the bound by the exact score
-            const int lid = a.li[off];
-            const uint64_t key = make_key(a.lv[off], lid);
-            if (lid >= 0 && lid < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
-          }
-          sids[j * kBlock + tid] = id;
-          if (id >= 0) batch_ovf = 1;
-        } else {
-          const int id = a.li ? a.li[off] : (int)((int64_t)lo * a.cap + idx);
-          const uint64_t key = make_key(a.lv[off], id);
-          if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
-        }
+        const int L = list_of(S, NL, gi);
+        const int idx = gi - S.pre[L];
+        const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
+        const int id = a.li ? a.li[off] : (int)((int64_t)L * a.cap + idx);
+        const uint64_t key = make_key(a.lv[off], id);
+        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
       }
     }
-    if (RESCORE) __syncthreads();
-    if (RESCORE && batch_ovf) {  // exact scores of the batch's overflow rows, 16 lanes per row
-      const int cnt = min(kBatch, total - base);
-      for (int c0 = (tid >> 4) * RU; c0 < cnt; c0 += (kBlock / 16) * RU) {
-        int idu[RU];
-        half8 xv[RU][RL];
-#pragma unroll
-        for (int u = 0; u < RU; ++u) idu[u] = c0 + u < cnt ? sids[c0 + u] : -1;
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-          const half8* xr = reinterpret_cast<const half8*>(a.x + (int64_t)(idu[u] < 0 ? 0 : idu[u]) * a.d);
-#pragma unroll
-          for (int m = 0; m < RL; ++m) {
-            const int c = l16 + 16 * m;
-            xv[u][m] = (idu[u] >= 0 && c < nd) ? xr[c] : half8{};
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-          float acc = 0.f;
-#pragma unroll
-          for (int m = 0; m < RL; ++m)
-#pragma unroll
-            for (int j = 0; j < 8; j += 2)
-              acc = __builtin_amdgcn_fdot2(half2v{qv[m][j], qv[m][j + 1]}, half2v{xv[u][m][j], xv[u][m][j + 1]}, acc,
-                                           false);
-#pragma unroll
-          for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-          if (l16 == 0 && idu[u] >= 0) {
-            const uint64_t key = make_key(acc, idu[u]);
-            if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    const int nb = S.nbuf;
-    const bool last = base + kBatch >= total;
-    if (nb > kBuf - kBatch || (last && nb > k)) {
-      const uint64_t kth = block_keep_top(S, nb, k);
-      if (tid == 0) {
-        S.nbuf = k;
-        S.thr_key = kth;
-      }
-      __syncthreads();
-    }
+    end_batch(S, k, base + kBatch >= total);
   }
 
   const int nb = min(S.nbuf, k);
-  if (MODE == kSelTau && quant)
-    q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
   if (MODE == kSelTau) {
+    if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
     // the k-th best key is the smallest survivor
     if (tid < kWave) {
       uint64_t m = ~0ull;
@@ -339,21 +374,175 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
       if (tid == 0) a.tau[q] = (nb >= k) ? key_score(m) : -__builtin_inff();
     }
   } else {
-    int N = 2;
-    while (N < nb) N <<= 1;
-    for (int i = nb + tid; i < N; i += kBlock) S.keys[i] = 0ull;
-    __syncthreads();
-    block_sort_desc(S.keys, N);
-    for (int r = tid; r < k; r += kBlock) {
-      const bool ok = r < nb;
-      a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
-      const int id = ok ? key_id(S.keys[r]) : -1;
-      if (a.ids64)
-        ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
-      else
-        ((int*)a.out_i)[(int64_t)q * k + r] = id;
+    write_topk(S, a, q, nb);
+  }
+}
+
+// Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
+// l, l+16, ... (RL of them at most); each group works on RU candidates at once,
+// so RL*RU independent loads per lane are in flight.  RL = 4 covers d <= 512,
+// RL = 6 d <= 768, RL = 12 (one candidate at a time) d <= 1536.
+template <int MODE>
+struct RescoreShape {
+  static constexpr int RL = MODE == kSelRescoreWide ? 12 : MODE == kSelRescoreMid ? 6 : 4;
+  static constexpr int RU = MODE == kSelRescoreWide ? 1 : MODE == kSelRescoreMid ? 2 : 4;
+};
+
+// Exact fp32 scores (v_dot2_f32_f16) of the rows sids[0..m) against the query
+// fragments qv; keys above t are appended to S.keys.  Whole block.
+template <int RL, int RU>
+__device__ __forceinline__ void rescore_rows(SelShared& S, const int* sids, int m, uint64_t t,
+                                             const half8 (&qv)[RL], const _Float16* x, int d) {
+  const int l16 = threadIdx.x & 15;
+  const int nd = d / 8;
+  for (int c0 = (threadIdx.x >> 4) * RU; c0 < m; c0 += (kBlock / 16) * RU) {
+    int idu[RU];
+    half8 xv[RU][RL];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) idu[u] = c0 + u < m ? sids[c0 + u] : -1;
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const half8* xr = reinterpret_cast<const half8*>(x + (int64_t)(idu[u] < 0 ? 0 : idu[u]) * d);
+#pragma unroll
+      for (int p = 0; p < RL; ++p) {
+        const int c = l16 + 16 * p;
+        xv[u][p] = (idu[u] >= 0 && c < nd) ? xr[c] : half8{};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      float acc = 0.f;
+#pragma unroll
+      for (int p = 0; p < RL; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2)
+          acc = __builtin_amdgcn_fdot2(half2v{qv[p][j], qv[p][j + 1]}, half2v{xv[u][p][j], xv[u][p][j + 1]}, acc,
+                                       false);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+      if (l16 == 0 && idu[u] >= 0) {
+        const uint64_t key = make_key(acc, idu[u]);
+        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+      }
     }
   }
+}
+
+// Final stage of the int8 pre-filter: the exact top-k of query blockIdx.x from
+// its candidate lists, whose entries are (U, row id) with U the scan's upper
+// bound of the row's score.  The scan's bound covers |S - A| plus three times
+// the rounding error eps of an fp32 sum of a row's products, so the score S'
+// recomputed here (|S' - S| <= eps) satisfies S' <= U.
+//
+// Phase 1 keeps the k candidates of largest U (keys (U, id)) and rescores
+// them; the smallest of their exact keys is a lower bound of the final k-th
+// best key, since they are k real rows.  Phase 2 rescores only the other
+// candidates whose U reaches the score of the running k-th best key: any
+// other has S' <= U below it and cannot enter.  (With ~400 candidates per
+// query at 1M rows, k = 10, about 70 rows are rescored instead of all.)
+// A list that overflowed in the scan (count > cap) stands for every row of
+// its range: those rows skip phase 1 and are all rescored in phase 2, so the
+// result stays exact whatever the data.
+//
+// With a.exact set, rescore_kernel has already replaced the bounds by exact
+// scores (small batches, where it spreads the row reads over more workgroups
+// than one per query): phase 1 is then a plain selection, and phase 2 only
+// rescans overflowed lists.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
+  __shared__ SelShared S;
+  constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
+  __shared__ int sids[kBatch];                    // rows to rescore
+  __shared__ unsigned ovf[kSelectMaxLists / 32];  // overflowed-list bitmap
+  __shared__ uint64_t red[kWaves];
+  __shared__ int nrows;
+  __shared__ int any_ovf;
+  const int tid = threadIdx.x;
+  const int q = blockIdx.x;
+  const int NL = a.nlists;
+  const int k = a.k;
+  const int l16 = tid & 15;
+  half8 qv[RL];
+  {
+    const int nd = a.d / 8;
+    const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
+#pragma unroll
+    for (int p = 0; p < RL; ++p) {
+      const int c = l16 + 16 * p;
+      qv[p] = c < nd ? qr[c] : half8{};
+    }
+  }
+  for (int i = tid; i < (NL + 31) / 32; i += kBlock) ovf[i] = 0u;
+  if (tid == 0) any_ovf = 0;
+  __syncthreads();
+  const int total = list_prefix(S, a, q, true, ovf, &any_ovf);
+  auto overflowed = [&](int L) { return ((ovf[L >> 5] >> (L & 31)) & 1u) != 0; };
+
+  // Phase 1: the k largest (U, id) keys of the lists that did not overflow.
+  for (int base = 0; base < total; base += kBatch) {
+    const uint64_t t = S.thr_key;
+    for (int j = 0; j < kBatch / kBlock; ++j) {
+      const int gi = base + j * kBlock + tid;
+      if (gi < total) {
+        const int L = list_of(S, NL, gi);
+        if (!overflowed(L)) {
+          const int64_t off = ((int64_t)q * NL + L) * a.cap + (gi - S.pre[L]);
+          const int id = a.li[off];
+          const uint64_t key = make_key(a.lv[off], id);
+          if (id >= 0 && id < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+        }
+      }
+    }
+    end_batch(S, k, base + kBatch >= total);
+  }
+  // Entries with a bound key below ucut are exactly those phase 1 did not keep.
+  uint64_t ucut = 0ull;
+  if (!a.exact) {  // (exact lists: the buffer already holds their best k keys)
+    const int n1 = S.nbuf;  // <= k
+    ucut = block_min_key(S.keys, n1, red);
+    for (int i = tid; i < n1; i += kBlock) sids[i] = key_id(S.keys[i]);
+    __syncthreads();
+    if (tid == 0) S.nbuf = 0;
+    __syncthreads();
+    rescore_rows<RL, RU>(S, sids, n1, 0ull, qv, a.x, a.d);
+    __syncthreads();
+    if (n1 >= k) {
+      const uint64_t kth = block_min_key(S.keys, S.nbuf, red);
+      if (tid == 0) S.thr_key = kth;
+    }
+    __syncthreads();
+  }
+
+  // Phase 2: the remaining candidates that can still enter, and overflow rows.
+  for (int base = 0; base < total && (any_ovf || !a.exact); base += kBatch) {
+    const uint64_t t = S.thr_key;
+    const float umin = t ? key_score(t) : -__builtin_inff();
+    if (tid == 0) nrows = 0;
+    __syncthreads();
+    for (int j = 0; j < kBatch / kBlock; ++j) {
+      const int gi = base + j * kBlock + tid;
+      if (gi < total) {
+        const int L = list_of(S, NL, gi);
+        const int idx = gi - S.pre[L];
+        int id = -1;
+        if (overflowed(L)) {  // row idx of the list's range
+          const int64_t tile = (int64_t)(L / a.rsplits) * a.tpc + idx / a.wave_rows;
+          const int64_t row = tile * a.tile_rows + (int64_t)(L % a.rsplits) * a.wave_rows + idx % a.wave_rows;
+          if (tile < a.ntiles && row < a.n) id = (int)row;
+        } else if (!a.exact) {
+          const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
+          const int lid = a.li[off];
+          const float u = a.lv[off];
+          if (lid >= 0 && lid < a.n && make_key(u, lid) < ucut && u >= umin) id = lid;
+        }
+        if (id >= 0) sids[atomicAdd(&nrows, 1)] = id;
+      }
+    }
+    __syncthreads();
+    rescore_rows<RL, RU>(S, sids, nrows, t, qv, a.x, a.d);
+    end_batch(S, k, base + kBatch >= total);
+  }
+  write_topk(S, a, q, min(S.nbuf, k));
 }
 
 // Exact scores of the int8 pre-filter's candidates, written over their bounds
@@ -515,26 +704,13 @@ __global__ __launch_bounds__(kBlock) void rowtopk_kernel(RowTopkArgs a) {
         pos = __shfl(pos, 0);
         if (pass) S.keys[pos + lanes_below(mk)] = key;
       }
-      __syncthreads();
-      const int nb = S.nbuf;
       const bool last = base + (sub + 1) * kBatch >= cnt;
-      if (nb > kBuf - kBatch || (last && nb > k)) {
-        const uint64_t kth = block_keep_top(S, nb, k);
-        if (tid == 0) {
-          S.nbuf = k;
-          S.thr_key = kth;
-        }
-        __syncthreads();
-      }
+      end_batch(S, k, last);
       if (last) break;
     }
   }
   const int nb = min(S.nbuf, k);
-  int N = 2;
-  while (N < nb) N <<= 1;
-  for (int i = nb + tid; i < N; i += kBlock) S.keys[i] = 0ull;
-  __syncthreads();
-  block_sort_desc(S.keys, N);
+  block_sort_keys(S.keys, nb);
   for (int r = tid; r < k; r += kBlock) {
     const bool ok = r < nb;
     const int64_t o = (int64_t)b * k + r;
@@ -563,6 +739,8 @@ hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s) {
   if (grid < 1 || grid > 0x7fffffff) return hipErrorInvalidValue;
   if (a.d <= 16 * 8 * RescoreShape<kSelRescore>::RL)
     hipLaunchKernelGGL(rescore_kernel<kSelRescore>, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+  else if (a.d <= 16 * 8 * RescoreShape<kSelRescoreMid>::RL)
+    hipLaunchKernelGGL(rescore_kernel<kSelRescoreMid>, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
   else
     hipLaunchKernelGGL(rescore_kernel<kSelRescoreWide>, dim3((unsigned)grid), dim3(kBlock), 0, s, a);
   return hipGetLastError();
@@ -586,9 +764,11 @@ hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
           (int64_t)a.tpc * a.wave_rows > 0x7fffffff)
         return hipErrorInvalidValue;
       if (a.d <= 16 * 8 * RescoreShape<kSelRescore>::RL)
-        hipLaunchKernelGGL(select_kernel<kSelRescore>, dim3(nq), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL(rescore_select_kernel<kSelRescore>, dim3(nq), dim3(kBlock), 0, s, a);
+      else if (a.d <= 16 * 8 * RescoreShape<kSelRescoreMid>::RL)
+        hipLaunchKernelGGL(rescore_select_kernel<kSelRescoreMid>, dim3(nq), dim3(kBlock), 0, s, a);
       else
-        hipLaunchKernelGGL(select_kernel<kSelRescoreWide>, dim3(nq), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL(rescore_select_kernel<kSelRescoreWide>, dim3(nq), dim3(kBlock), 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;

@@ -29,14 +29,18 @@ _NORM_CHUNK = 1 << 18
 # rows; exact results).  Built by default for corpora of at least Q8_MIN_ROWS
 # rows wider than Q8_MIN_WIDTH; "auto" uses it where it measured faster than the
 # fp16 scan (MI355X latency grid, 100k-4M rows x 384/768, k 10/100, batch
-# 1/32/256): batch 1 (bandwidth-bound GEMV on half the bytes), and over at least
-# Q8_BATCH_MIN_ROWS rows batches of at most Q8_MAX_BATCH queries or with
-# k <= Q8_MAX_K.  (Large batches with large k stay on the fp16 path: the int8
-# bound lets through ~3x the candidates, each an fp16 row read.)
+# 1-256): batch 1 (bandwidth-bound GEMV on half the bytes), and over at least
+# Q8_BATCH_MIN_ROWS rows any batch with k <= Q8_MAX_K, batches of at most
+# Q8_MAX_BATCH queries, and batches of at least Q8_TWO_PHASE_BATCH (where the
+# select rescores the k candidates of largest bound first and then only those
+# that can still enter).  Batches in between with larger k stay on the fp16
+# path: there every candidate that passes the int8 bound (~3x the fp16 scan's)
+# is rescored from its fp16 row.
 Q8_MIN_ROWS = 1 << 18
 Q8_MIN_WIDTH = 256
 Q8_MAX_K = 16
 Q8_MAX_BATCH = 64
+Q8_TWO_PHASE_BATCH = 160
 Q8_BATCH_MIN_ROWS = 1 << 19
 
 METHODS = ("auto", "fused", "twopass", "torch", "int8")
@@ -218,7 +222,8 @@ class Index:
         """Whether "auto" sends a batch of nq queries with this k to the int8 path."""
         if self._xq is None or k > MAX_FUSED_K:
             return False
-        return nq == 1 or (len(self) >= Q8_BATCH_MIN_ROWS and (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH))
+        return nq == 1 or (len(self) >= Q8_BATCH_MIN_ROWS and
+                           (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH or nq >= Q8_TWO_PHASE_BATCH))
 
     def _search_large_k(self, q: torch.Tensor, k: int):
         """Exact top-k for MAX_FUSED_K < k <= MAX_EXACT_K on the GPU: fp32 score

@@ -549,6 +549,40 @@ def test_q8_overflowing_lists_are_rescanned(eng):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nq,k", [(1, 10), (64, 100), (160, 10), (160, 100)])
+def test_q8_loose_bounds_reorder_candidates(eng, nq, k):
+    """Blocks holding one very long row get a coarse int8 scale, so their other
+    rows carry score bounds near 1 while their exact scores are ordinary: the k
+    candidates of largest bound, which the select rescores first, are not the
+    top k, and the exact result has to come from the remaining candidates.
+    Batches below 128 rescore every candidate before the select; from 128 on
+    the select rescores the k of largest bound first, then only the rest that
+    can still enter."""
+    say(f"q8 loose bounds nq={nq} k={k}")
+    x, q = make(40000, 384, nq, seed=17 + nq + k)
+    for blk in (10, 150, 300, 450, 600):
+        x[blk * 64] = 0
+        x[blk * 64, blk % 384] = 30.0
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    v8, i8, v, i = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64), v.cpu().numpy(), i.cpu().numpy()
+    # a missed row would open a gap in the sorted scores; ids may differ only
+    # between rows whose fp32 scores agree to the rounding of the sum order
+    np.testing.assert_allclose(v8, v, rtol=0, atol=2e-6)
+    same = i8 == i
+    say(f"  id mismatches {int((~same).sum())}")
+    assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
+    assert oracle.check_exact(q.numpy(), x.numpy(), k, v8, i8) >= 0.99
+    # the loose blocks' ordinary rows are not what the search returns
+    loose = {blk * 64 + r for blk in (10, 150, 300, 450, 600) for r in range(1, 64)}
+    assert np.isin(i8, list(loose)).mean() < 0.2
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("flags", [_ext.FLAG_NO_PREPASS, _ext.FLAG_FORCE_PREPASS, _ext.FLAG_IDS_INT64,
                                    _ext.FLAG_NO_GEMV])
 def test_q8_flags(eng, flags):
@@ -614,7 +648,8 @@ def test_index_auto_int8_at_size_is_exact():
     x, q = make(n, 384, 8, seed=5)
     idx = Index(x, metric="ip")
     assert idx._xq is not None and idx._int8_wins(8, 10) and idx._int8_wins(8, 100)
-    assert idx._int8_wins(256, 16) and not idx._int8_wins(256, 100) and not idx._int8_wins(8, 300)
+    assert idx._int8_wins(256, 16) and idx._int8_wins(256, 100) and idx._int8_wins(64, 100)
+    assert not idx._int8_wins(128, 100) and not idx._int8_wins(8, 300)
     v, i = idx.search(q, 10)
     vf, i_f = idx.search(q, 10, method="fused")
     assert torch.equal(i, i_f)
