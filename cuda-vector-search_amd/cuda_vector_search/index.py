@@ -51,10 +51,15 @@ def int8_builds(n: int, width: int) -> bool:
     return n >= Q8_MIN_ROWS and Q8_MIN_WIDTH < width <= MAX_KERNEL_WIDTH
 
 
+def _int8_faster(n: int, nq: int, k: int) -> bool:
+    """Whether the int8 path measured faster than the fp16 scan for this shape."""
+    return k <= MAX_FUSED_K and (nq == 1 or (n >= Q8_BATCH_MIN_ROWS and (
+        k <= Q8_MAX_K or nq <= Q8_MAX_BATCH or nq >= Q8_TWO_PHASE_BATCH)))
+
+
 def int8_auto(n: int, width: int, nq: int, k: int) -> bool:
     """Whether method="auto" runs the int8 path (default companion, k <= 256)."""
-    return int8_builds(n, width) and k <= MAX_FUSED_K and (
-        nq == 1 or (n >= Q8_BATCH_MIN_ROWS and (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH)))
+    return int8_builds(n, width) and _int8_faster(n, nq, k)
 
 
 def q8_row_bytes(width: int) -> int:
@@ -220,10 +225,7 @@ class Index:
 
     def _int8_wins(self, nq: int, k: int) -> bool:
         """Whether "auto" sends a batch of nq queries with this k to the int8 path."""
-        if self._xq is None or k > MAX_FUSED_K:
-            return False
-        return nq == 1 or (len(self) >= Q8_BATCH_MIN_ROWS and
-                           (k <= Q8_MAX_K or nq <= Q8_MAX_BATCH or nq >= Q8_TWO_PHASE_BATCH))
+        return self._xq is not None and _int8_faster(len(self), nq, k)
 
     def _search_large_k(self, q: torch.Tensor, k: int):
         """Exact top-k for MAX_FUSED_K < k <= MAX_EXACT_K on the GPU: fp32 score

@@ -31,10 +31,10 @@ def test_dominant_kernel_patterns_match_the_append_launches_only():
 
 
 def test_dominant_kernel_follows_the_auto_path():
-    # C2 (1M x 384, b256, k10) and C3 (b1) take the int8 pre-filter; C1 (100k
-    # rows), C4 and C5 (k=100) the fp16 fused path
+    # C2 (1M x 384, b256, k10), C3 (b1) and C4 (1M x 768, b256, k100) take the
+    # int8 pre-filter; C1 and C5 (100k rows) the fp16 fused path
     assert [bench.dominant_key(c) for c in ("C1", "C2", "C3", "C4", "C5")] == \
-        ["scan", "scan_q8", "gemv_q8", "scan", "scan"]
+        ["scan", "scan_q8", "gemv_q8", "scan_q8", "scan"]
 
 
 def test_instantiated_kernels_are_the_ones_the_patterns_expect():
