@@ -34,6 +34,7 @@ namespace {
 constexpr int kBuf = 4096;    // LDS key buffer
 constexpr int kBatch = 2048;  // candidates gathered per round
 constexpr int kWaves = kBlock / kWave;
+constexpr int kGather = kBatch / kBlock;  // entries per thread per round
 
 template <int MAXL>
 struct SelSharedT {
@@ -348,16 +349,28 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int total = list_prefix(S, a, q, false);
   for (int base = 0; base < total; base += kBatch) {
     const uint64_t t = S.thr_key;
-    for (int j = 0; j < kBatch / kBlock; ++j) {
+    // all of this thread's list lookups and loads first, then the appends: an
+    // append (an LDS store) would otherwise order every later lookup after it
+    // and expose one memory latency per entry
+    float val[kGather];
+    int idv[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
       const int gi = base + j * kBlock + tid;
+      val[j] = 0.f;
+      idv[j] = 0;
       if (gi < total) {
         const int L = list_of(S, NL, gi);
         const int idx = gi - S.pre[L];
         const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
-        const int id = a.li ? a.li[off] : (int)((int64_t)L * a.cap + idx);
-        const uint64_t key = make_key(a.lv[off], id);
-        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+        idv[j] = a.li ? a.li[off] : (int)((int64_t)L * a.cap + idx);
+        val[j] = a.lv[off];
       }
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const uint64_t key = make_key(val[j], idv[j]);
+      if (base + j * kBlock + tid < total && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
     }
     end_batch(S, k, base + kBatch >= total);
   }
@@ -481,17 +494,26 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
   // Phase 1: the k largest (U, id) keys of the lists that did not overflow.
   for (int base = 0; base < total; base += kBatch) {
     const uint64_t t = S.thr_key;
-    for (int j = 0; j < kBatch / kBlock; ++j) {
+    float val[kGather];
+    int idv[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {  // lookups and loads first (see select_kernel)
       const int gi = base + j * kBlock + tid;
+      val[j] = 0.f;
+      idv[j] = -1;
       if (gi < total) {
         const int L = list_of(S, NL, gi);
         if (!overflowed(L)) {
           const int64_t off = ((int64_t)q * NL + L) * a.cap + (gi - S.pre[L]);
-          const int id = a.li[off];
-          const uint64_t key = make_key(a.lv[off], id);
-          if (id >= 0 && id < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+          idv[j] = a.li[off];
+          val[j] = a.lv[off];
         }
       }
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const uint64_t key = make_key(val[j], idv[j]);
+      if (idv[j] >= 0 && idv[j] < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
     }
     end_batch(S, k, base + kBatch >= total);
   }
@@ -519,25 +541,29 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
     const float umin = t ? key_score(t) : -__builtin_inff();
     if (tid == 0) nrows = 0;
     __syncthreads();
-    for (int j = 0; j < kBatch / kBlock; ++j) {
+    int idv[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {  // lookups and loads first (see select_kernel)
       const int gi = base + j * kBlock + tid;
+      idv[j] = -1;
       if (gi < total) {
         const int L = list_of(S, NL, gi);
         const int idx = gi - S.pre[L];
-        int id = -1;
         if (overflowed(L)) {  // row idx of the list's range
           const int64_t tile = (int64_t)(L / a.rsplits) * a.tpc + idx / a.wave_rows;
           const int64_t row = tile * a.tile_rows + (int64_t)(L % a.rsplits) * a.wave_rows + idx % a.wave_rows;
-          if (tile < a.ntiles && row < a.n) id = (int)row;
+          if (tile < a.ntiles && row < a.n) idv[j] = (int)row;
         } else if (!a.exact) {
           const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
           const int lid = a.li[off];
           const float u = a.lv[off];
-          if (lid >= 0 && lid < a.n && make_key(u, lid) < ucut && u >= umin) id = lid;
+          if (lid >= 0 && lid < a.n && make_key(u, lid) < ucut && u >= umin) idv[j] = lid;
         }
-        if (id >= 0) sids[atomicAdd(&nrows, 1)] = id;
       }
     }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j)
+      if (idv[j] >= 0) sids[atomicAdd(&nrows, 1)] = idv[j];
     __syncthreads();
     rescore_rows<RL, RU>(S, sids, nrows, t, qv, a.x, a.d);
     end_batch(S, k, base + kBatch >= total);
@@ -607,16 +633,30 @@ __global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
     const int cnt = min(kBatch, total - base);
     // every id of the batch is read before any survivor is written back, and a
     // survivor's new slot never passes an unread entry of its list
-    for (int i = tid; i < cnt; i += kBlock) {
-      const int gi = base + i;
-      int lo = 0, hi = nl;  // largest list with pre[list] <= gi
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (pre[mid] <= gi) lo = mid; else hi = mid;
+    int idv[kGather], lov[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {  // lookups and loads first (see select_kernel)
+      const int i = j * kBlock + tid;
+      idv[j] = -1;
+      lov[j] = 0;
+      if (i < cnt) {
+        const int gi = base + i;
+        int lo = 0, hi = nl;  // largest list with pre[list] <= gi
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (pre[mid] <= gi) lo = mid; else hi = mid;
+        }
+        idv[j] = liq[(int64_t)lo * a.cap + (gi - pre[lo])];
+        lov[j] = lo;
       }
-      const int id = liq[(int64_t)lo * a.cap + (gi - pre[lo])];
-      sid[i] = (id >= 0 && id < a.n) ? id : -1;
-      slist[i] = (short)lo;
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const int i = j * kBlock + tid;
+      if (i < cnt) {
+        sid[i] = (idv[j] >= 0 && idv[j] < a.n) ? idv[j] : -1;
+        slist[i] = (short)lov[j];
+      }
     }
     __syncthreads();
     for (int c0 = (tid >> 4) * RU; c0 < cnt; c0 += (kBlock / 16) * RU) {
