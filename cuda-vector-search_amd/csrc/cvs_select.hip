@@ -391,6 +391,93 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
 }
 
+// Loose cut of the buffer's keys by score: a 256-bin histogram over the
+// scores' [min, max] picks the fewest top bins holding at least k keys, and
+// every key in them (m >= k keys, exactly those >= the returned key) is kept,
+// compacted to keys[0..m).  Seven barriers, where the exact radix cut needs
+// three or four per 8-bit digit.  Returns 0 and leaves the buffer alone when
+// m would exceed `limit` (many keys sharing a score).  Whole block; nb > k.
+__device__ uint64_t block_cut_hist(SelShared& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
+  constexpr int PER = kBuf / kBlock;
+  __shared__ float mm[2][kWaves];
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  const int lane = tid % kWave;
+  uint64_t r[PER];
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = j * kBlock + tid;
+    r[j] = i < nb ? S.keys[i] : 0ull;
+    if (i < nb) {
+      const float v = key_score(r[j]);
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off));
+    hi = fmaxf(hi, __shfl_xor(hi, off));
+  }
+  if (lane == 0) {
+    mm[0][w] = lo;
+    mm[1][w] = hi;
+  }
+  for (int i = tid; i < kWaves * 256; i += kBlock) (&S.hist[0][0])[i] = 0;
+  __syncthreads();
+  lo = mm[0][0];
+  hi = mm[1][0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    lo = fminf(lo, mm[0][i]);
+    hi = fmaxf(hi, mm[1][i]);
+  }
+  // bin(score): non-decreasing in the score, the same arithmetic everywhere
+  const float scale = hi > lo ? 256.0f / (hi - lo) : 0.0f;
+  auto bin = [&](uint64_t key) { return min(255, max(0, (int)((key_score(key) - lo) * scale))); };
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (j * kBlock + tid < nb) atomicAdd(&S.hist[w][bin(r[j])], 1);
+  __syncthreads();
+  if (w == 0) {  // the highest bin b with #(keys in bins >= b) >= k
+    int c[4];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
+      const int b = 255 - (4 * lane + j);
+      c[j] = S.hist[0][b] + S.hist[1][b] + S.hist[2][b] + S.hist[3][b];
+      sum += c[j];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int o = __shfl_up(incl, off);
+      if (lane >= off) incl += o;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (run < k && k <= run + c[j]) {
+        S.digit = 255 - (4 * lane + j);
+        S.above = run + c[j];
+      }
+      run += c[j];
+    }
+    if (lane == 0) S.ncut = 0;
+  }
+  __syncthreads();
+  const int bstar = S.digit;
+  const int m = S.above;
+  *m_out = m;
+  if (m > limit) return 0ull;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (j * kBlock + tid < nb && bin(r[j]) >= bstar) S.keys[atomicAdd(&S.ncut, 1)] = r[j];
+  __syncthreads();
+  return block_min_key(S.keys, m, red);
+}
+
 // Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
 // l, l+16, ... (RL of them at most); each group works on RU candidates at once,
 // so RL*RU independent loads per lane are in flight.  RL = 4 covers d <= 512,
@@ -515,20 +602,50 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
       const uint64_t key = make_key(val[j], idv[j]);
       if (idv[j] >= 0 && idv[j] < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
     }
-    end_batch(S, k, base + kBatch >= total);
+    const bool last = base + kBatch >= total;
+    if (a.exact) {
+      end_batch(S, k, last);
+    } else {
+      // bound keys: any m >= k of the largest serve phase 1, so a loose cut
+      // (at most kBlock keys after the last one) replaces the radix cut
+      __syncthreads();
+      const int nb = S.nbuf;
+      if (nb > kBuf - kBatch || (last && nb > k)) {
+        int m = 0;
+        uint64_t cut = block_cut_hist(S, nb, k, last ? kBlock : kBuf - kBatch, red, &m);
+        if (m > (last ? kBlock : kBuf - kBatch)) {
+          cut = block_keep_top(S, nb, k);
+          m = k;
+        }
+        if (tid == 0) {
+          S.nbuf = m;
+          S.thr_key = cut - 1;  // keep appending keys >= cut (a real key, > 0)
+        }
+      }
+      __syncthreads();
+    }
   }
   // Entries with a bound key below ucut are exactly those phase 1 did not keep.
   uint64_t ucut = 0ull;
   if (!a.exact) {  // (exact lists: the buffer already holds their best k keys)
-    const int n1 = S.nbuf;  // <= k
+    const int n1 = S.nbuf;  // <= k, or m <= kBlock after a loose cut
     ucut = block_min_key(S.keys, n1, red);
     for (int i = tid; i < n1; i += kBlock) sids[i] = key_id(S.keys[i]);
     __syncthreads();
-    if (tid == 0) S.nbuf = 0;
+    if (tid == 0) {
+      S.nbuf = 0;
+      S.thr_key = 0ull;
+    }
     __syncthreads();
     rescore_rows<RL, RU>(S, sids, n1, 0ull, qv, a.x, a.d);
     __syncthreads();
-    if (n1 >= k) {
+    if (n1 > k) {  // n1 <= kBlock: sort, keep the k best
+      block_rank_sort(S.keys, S.nbuf);
+      if (tid == 0) {
+        S.nbuf = k;
+        S.thr_key = S.keys[k - 1];
+      }
+    } else if (n1 == k) {
       const uint64_t kth = block_min_key(S.keys, S.nbuf, red);
       if (tid == 0) S.thr_key = kth;
     }
