@@ -583,6 +583,33 @@ def test_q8_loose_bounds_reorder_candidates(eng, nq, k):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("k", [10, 100])
+def test_q8_equal_bounds_fall_back_to_the_exact_cut(eng, k):
+    """Six 64-row blocks made of copies of query 0's row, far apart: 384
+    candidates in ordinary lists (none overflows) share one score bound, so the
+    select's histogram cut cannot isolate k of them and takes the exact cut;
+    the result is the k copies of smallest id."""
+    say(f"q8 equal bounds k={k}")
+    x, q = make(40000, 384, 160, seed=23 + k)
+    blocks = (20, 140, 260, 380, 500, 620)
+    for blk in blocks:
+        x[blk * 64:(blk + 1) * 64] = q[0]
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    v8, i8, v, i = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64), v.cpu().numpy(), i.cpu().numpy()
+    copies = [blk * 64 + r for blk in blocks for r in range(64)]
+    assert i8[0].tolist() == copies[:k]
+    np.testing.assert_allclose(v8, v, rtol=0, atol=2e-6)
+    same = i8 == i
+    assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
+    oracle.check_exact(q.numpy(), x.numpy(), k, v8, i8)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("flags", [_ext.FLAG_NO_PREPASS, _ext.FLAG_FORCE_PREPASS, _ext.FLAG_IDS_INT64,
                                    _ext.FLAG_NO_GEMV])
 def test_q8_flags(eng, flags):
