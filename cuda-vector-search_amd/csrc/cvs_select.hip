@@ -271,31 +271,6 @@ __device__ __forceinline__ int list_of(const SH& S, int NL, int gi) {
   return lo;
 }
 
-// End of a batch of appends: cuts the buffer to its k best keys (raising the
-// threshold key) when the next batch might not fit, or when this batch was the
-// last (a last buffer of at most kBlock keys is sorted instead, leaving its k
-// best first).  Whole block.  Every thread reads the count before any thread can
-// append again, so all take the same branch.
-template <class SH>
-__device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
-  __syncthreads();
-  const int nb = S.nbuf;
-  if (last && nb <= kBlock) {  // small: sort it outright and keep the first k
-    block_rank_sort(S.keys, nb);
-    if (threadIdx.x == 0 && nb > k) {
-      S.nbuf = k;
-      S.thr_key = S.keys[k - 1];
-    }
-  } else if (nb > kBuf - kBatch || (last && nb > k)) {
-    const uint64_t kth = block_keep_top(S, nb, k);
-    if (threadIdx.x == 0) {
-      S.nbuf = k;
-      S.thr_key = kth;
-    }
-  }
-  __syncthreads();
-}
-
 // Smallest of keys[0..nb) (~0 when nb == 0).  Whole block; `red` is kWaves
 // words of LDS.
 __device__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
@@ -313,91 +288,14 @@ __device__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
   return r;
 }
 
-// Sorts the nb (<= k) surviving keys and writes row q of the outputs, padded
-// with (-inf, -1).  Whole block.
-__device__ void write_topk(SelShared& S, const SelectArgs& a, int q, int nb) {
-  const int tid = threadIdx.x;
-  const int k = a.k;
-  block_sort_keys(S.keys, nb);
-  for (int r = tid; r < k; r += kBlock) {
-    const bool ok = r < nb;
-    a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
-    const int id = ok ? key_id(S.keys[r]) : -1;
-    if (a.ids64)
-      ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
-    else
-      ((int*)a.out_i)[(int64_t)q * k + r] = id;
-  }
-}
-
-// Final and threshold modes: query blockIdx.x's candidate keys are streamed
-// through the LDS buffer in kBatch steps, each filtered against the running
-// k-th best key.
-template <int MODE>
-__global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
-  __shared__ SelShared S;
-  const int tid = threadIdx.x;
-  const int q = blockIdx.x;
-  const int NL = a.nlists;
-  const int k = a.k;
-  // int8 pre-filter: wave 1 loads this query's row now and quantises it after
-  // the selection (the load latency hides behind the selection's work)
-  float qrow[kQ8RowPer];  // (dead outside the threshold mode)
-  const bool quant = MODE == kSelTau && a.qq_out != nullptr && tid >= kWave && tid < 2 * kWave;
-  if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
-
-  const int total = list_prefix(S, a, q, false);
-  for (int base = 0; base < total; base += kBatch) {
-    const uint64_t t = S.thr_key;
-    // all of this thread's list lookups and loads first, then the appends: an
-    // append (an LDS store) would otherwise order every later lookup after it
-    // and expose one memory latency per entry
-    float val[kGather];
-    int idv[kGather];
-#pragma unroll
-    for (int j = 0; j < kGather; ++j) {
-      const int gi = base + j * kBlock + tid;
-      val[j] = 0.f;
-      idv[j] = 0;
-      if (gi < total) {
-        const int L = list_of(S, NL, gi);
-        const int idx = gi - S.pre[L];
-        const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
-        idv[j] = a.li ? a.li[off] : (int)((int64_t)L * a.cap + idx);
-        val[j] = a.lv[off];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kGather; ++j) {
-      const uint64_t key = make_key(val[j], idv[j]);
-      if (base + j * kBlock + tid < total && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
-    }
-    end_batch(S, k, base + kBatch >= total);
-  }
-
-  const int nb = min(S.nbuf, k);
-  if (MODE == kSelTau) {
-    if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
-    // the k-th best key is the smallest survivor
-    if (tid < kWave) {
-      uint64_t m = ~0ull;
-      for (int i = tid; i < nb; i += kWave) m = min(m, S.keys[i]);
-#pragma unroll
-      for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
-      if (tid == 0) a.tau[q] = (nb >= k) ? key_score(m) : -__builtin_inff();
-    }
-  } else {
-    write_topk(S, a, q, nb);
-  }
-}
-
 // Loose cut of the buffer's keys by score: a 256-bin histogram over the
 // scores' [min, max] picks the fewest top bins holding at least k keys, and
 // every key in them (m >= k keys, exactly those >= the returned key) is kept,
 // compacted to keys[0..m).  Seven barriers, where the exact radix cut needs
 // three or four per 8-bit digit.  Returns 0 and leaves the buffer alone when
 // m would exceed `limit` (many keys sharing a score).  Whole block; nb > k.
-__device__ uint64_t block_cut_hist(SelShared& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
+template <class SH>
+__device__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
   constexpr int PER = kBuf / kBlock;
   __shared__ float mm[2][kWaves];
   const int tid = threadIdx.x;
@@ -476,6 +374,151 @@ __device__ uint64_t block_cut_hist(SelShared& S, int nb, int k, int limit, uint6
     if (j * kBlock + tid < nb && bin(r[j]) >= bstar) S.keys[atomicAdd(&S.ncut, 1)] = r[j];
   __syncthreads();
   return block_min_key(S.keys, m, red);
+}
+
+// End of a batch of appends.  When the next batch might not fit, the buffer is
+// cut to the keys of its top histogram bins (at least k, raising the threshold
+// key), or to exactly its k best when those bins hold too many.  After the last
+// batch the buffer is cut to at most kBlock keys that hold its k best the same
+// way and sorted by rank, leaving the k best first.  Whole block.  Every thread
+// reads the count before any thread can append again, so all take the same
+// branch.
+template <bool HIST = true, class SH>
+__device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
+  __shared__ uint64_t red[kWaves];
+  __syncthreads();
+  int nb = S.nbuf;
+  if (!HIST) {  // exact cuts only (the row top-k: large k, registers needed elsewhere)
+    if (last && nb <= kBlock) {
+      block_rank_sort(S.keys, nb);
+      if (threadIdx.x == 0 && nb > k) {
+        S.nbuf = k;
+        S.thr_key = S.keys[k - 1];
+      }
+    } else if (nb > kBuf - kBatch || (last && nb > k)) {
+      const uint64_t kth = block_keep_top(S, nb, k);
+      if (threadIdx.x == 0) {
+        S.nbuf = k;
+        S.thr_key = kth;
+      }
+    }
+  } else if (!last && nb > kBuf - kBatch) {  // make room: a loose cut, else the exact one
+    int m = 0;
+    const uint64_t cut = block_cut_hist(S, nb, k, kBuf - kBatch, red, &m);
+    if (m <= kBuf - kBatch) {
+      if (threadIdx.x == 0) {
+        S.nbuf = m;
+        S.thr_key = cut - 1;  // keys >= cut (a real key, > 0) may still enter
+      }
+    } else {
+      const uint64_t kth = block_keep_top(S, nb, k);
+      if (threadIdx.x == 0) {
+        S.nbuf = k;
+        S.thr_key = kth;
+      }
+    }
+  } else if (last && nb > k) {
+    uint64_t kth = 0ull;
+    if (nb > kBlock) {  // down to at most kBlock keys holding the k best
+      int m = 0;
+      block_cut_hist(S, nb, k, kBlock, red, &m);
+      if (m > kBlock) {
+        kth = block_keep_top(S, nb, k);
+        m = k;
+      }
+      nb = m;
+    }
+    if (nb <= kBlock) {
+      block_rank_sort(S.keys, nb);  // sorted: the k best first
+      if (threadIdx.x == 0) {
+        S.nbuf = k;
+        S.thr_key = S.keys[k - 1];
+      }
+    } else if (threadIdx.x == 0) {  // k > kBlock: the exact cut's k keys, unsorted
+      S.nbuf = k;
+      S.thr_key = kth;
+    }
+  }
+  __syncthreads();
+}
+
+
+// Sorts the nb (<= k) surviving keys and writes row q of the outputs, padded
+// with (-inf, -1).  Whole block.
+__device__ void write_topk(SelShared& S, const SelectArgs& a, int q, int nb) {
+  const int tid = threadIdx.x;
+  const int k = a.k;
+  block_sort_keys(S.keys, nb);
+  for (int r = tid; r < k; r += kBlock) {
+    const bool ok = r < nb;
+    a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
+    const int id = ok ? key_id(S.keys[r]) : -1;
+    if (a.ids64)
+      ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
+    else
+      ((int*)a.out_i)[(int64_t)q * k + r] = id;
+  }
+}
+
+// Final and threshold modes: query blockIdx.x's candidate keys are streamed
+// through the LDS buffer in kBatch steps, each filtered against the running
+// k-th best key.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
+  __shared__ SelShared S;
+  const int tid = threadIdx.x;
+  const int q = blockIdx.x;
+  const int NL = a.nlists;
+  const int k = a.k;
+  // int8 pre-filter: wave 1 loads this query's row now and quantises it after
+  // the selection (the load latency hides behind the selection's work)
+  float qrow[kQ8RowPer];  // (dead outside the threshold mode)
+  const bool quant = MODE == kSelTau && a.qq_out != nullptr && tid >= kWave && tid < 2 * kWave;
+  if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
+
+  const int total = list_prefix(S, a, q, false);
+  for (int base = 0; base < total; base += kBatch) {
+    const uint64_t t = S.thr_key;
+    // all of this thread's list lookups and loads first, then the appends: an
+    // append (an LDS store) would otherwise order every later lookup after it
+    // and expose one memory latency per entry
+    float val[kGather];
+    int idv[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const int gi = base + j * kBlock + tid;
+      val[j] = 0.f;
+      idv[j] = 0;
+      if (gi < total) {
+        const int L = list_of(S, NL, gi);
+        const int idx = gi - S.pre[L];
+        const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
+        idv[j] = a.li ? a.li[off] : (int)((int64_t)L * a.cap + idx);
+        val[j] = a.lv[off];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const uint64_t key = make_key(val[j], idv[j]);
+      if (base + j * kBlock + tid < total && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+    }
+    end_batch(S, k, base + kBatch >= total);
+  }
+
+  const int nb = min(S.nbuf, k);
+  if (MODE == kSelTau) {
+    if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
+    // the k-th best key is the smallest survivor
+    if (tid < kWave) {
+      uint64_t m = ~0ull;
+      for (int i = tid; i < nb; i += kWave) m = min(m, S.keys[i]);
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
+      if (tid == 0) a.tau[q] = (nb >= k) ? key_score(m) : -__builtin_inff();
+    }
+  } else {
+    write_topk(S, a, q, nb);
+  }
 }
 
 // Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
@@ -862,7 +905,7 @@ __global__ __launch_bounds__(kBlock) void rowtopk_kernel(RowTopkArgs a) {
         if (pass) S.keys[pos + lanes_below(mk)] = key;
       }
       const bool last = base + (sub + 1) * kBatch >= cnt;
-      end_batch(S, k, last);
+      end_batch<false>(S, k, last);
       if (last) break;
     }
   }
