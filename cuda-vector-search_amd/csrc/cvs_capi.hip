@@ -415,6 +415,8 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       pa.nsample = (int)P.nsample;
       pa.spt = (int)P.spt;
       pa.agg = P.agg;
+      // two query groups of one sampled chunk on one XCD: its rows come from HBM once
+      pa.xcd_pair = (P.groups > 1 && P.nsample % 8 == 0) ? 1 : 0;
       pa.units = (int)P.units;
       e = launch_scan(P.cfg, kMax, pa, (int)(P.groups * P.nsample), s);
       if (e != hipSuccess) return hip_fail(e, "sample pass launch");
@@ -895,6 +897,8 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       pa.nsample = (int)S.nsample;
       pa.spt = (int)S.spt;
       pa.agg = S.agg;
+      // two query groups of one sampled chunk on one XCD: its rows come from HBM once
+      pa.xcd_pair = (S.groups > 1 && S.nsample % 8 == 0) ? 1 : 0;
       pa.units = (int)S.units;
       e = launch_scan(S.cfg, kMax, pa, (int)(S.groups * S.nsample), s);
     }

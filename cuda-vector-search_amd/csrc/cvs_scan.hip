@@ -169,7 +169,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   int grp, chunk;
   {
     const int id = blockIdx.x;
-    if (MODE != kMax && a.xcd_pair) {
+    if (a.xcd_pair) {  // (kMax: chunk = sampling workgroup, nsample % 8 == 0)
       const int slot = id >> 3;
       grp = slot % a.groups;
       chunk = (slot / a.groups) * 8 + (id & 7);
