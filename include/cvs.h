@@ -159,9 +159,11 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
  * calls as cvs_fused_topk, index.py:123-126, with half the corpus bytes
  * scanned).  An int8 companion of the corpus, built once, is scanned with int8
  * MFMAs; every row whose score upper bound (int8 score + a rigorous
- * quantisation-error bound) reaches the sampled threshold is kept, and the
- * select kernel recomputes those rows' exact fp16 scores.  Results are those of
- * cvs_fused_topk (same order, same ids, fp32-accumulated scores).
+ * quantisation-error bound) reaches the sampled threshold is a candidate, and
+ * exact fp16 scores are recomputed for the candidates that can still be in the
+ * top k (the bound of the rest is below the k-th best exact score found).
+ * Results are those of cvs_fused_topk (same order, same ids, fp32-accumulated
+ * scores).
  *
  * cvs_q8_corpus_bytes: size of the companion of an [n, d] corpus (int8 rows of
  *   384, 768 or 1536 bytes, the smallest that holds d, plus 16 bytes per
