@@ -251,6 +251,27 @@ def test_prepass_does_not_change_results(eng, flags, n, d, b, k):
     np.testing.assert_array_equal(i, i0)
 
 
+@pytest.mark.parametrize("k", [10, 100])
+def test_two_group_sampling_on_paired_xcds(eng, k):
+    """d = 768 at b = 256 runs two 128-query groups; with 128 sampling
+    workgroups per group (a multiple of 8) the sampling pass maps both groups
+    of a chunk to one XCD, on the fp16 and the int8 path alike."""
+    n, d, b = 200000, 768, 256
+    say(f"paired sampling n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=31 + k)
+    v, i, plan = run_fused(eng, q, x, k)
+    assert plan[0] == 128
+    assert oracle.check_exact(q, x, k, v, i) >= 0.999
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    v8, i8, _ = eng.q8_topk(qd, xd, eng.q8_build(xd), k)
+    torch.cuda.synchronize()
+    v8, i8 = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64)
+    np.testing.assert_allclose(v8, v, rtol=0, atol=2e-6)
+    same = i8 == i
+    assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
+
+
 @pytest.mark.parametrize("n,d,b,k", [(50000, 384, 256, 10), (70000, 768, 1, 10)])
 def test_timed_and_marked_twins_match(eng, n, d, b, k):
     """The diagnostic entry points run the same launches as fused_topk: identical
