@@ -331,9 +331,15 @@ __device__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* re
     lo = fminf(lo, mm[0][i]);
     hi = fmaxf(hi, mm[1][i]);
   }
-  // bin(score): non-decreasing in the score, the same arithmetic everywhere
-  const float scale = hi > lo ? 256.0f / (hi - lo) : 0.0f;
-  auto bin = [&](uint64_t key) { return min(255, max(0, (int)((key_score(key) - lo) * scale))); };
+  // bin(score): non-decreasing in the score, the same arithmetic everywhere, and
+  // in [0, 255] whatever the scores (infinite or NaN ones land in bin 0 or 255,
+  // and no out-of-range float reaches the integer conversion)
+  const bool span = hi > lo && __builtin_isfinite(lo) && __builtin_isfinite(hi);
+  const float scale = span ? 256.0f / (hi - lo) : 0.0f;
+  auto bin = [&](uint64_t key) {
+    const float t = (key_score(key) - lo) * scale;
+    return (int)(t >= 0.0f ? fminf(t, 255.0f) : 0.0f);
+  };
 #pragma unroll
   for (int j = 0; j < PER; ++j)
     if (j * kBlock + tid < nb) atomicAdd(&S.hist[w][bin(r[j])], 1);
