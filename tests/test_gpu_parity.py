@@ -467,6 +467,26 @@ def test_topk_rows_matches_sorted_rows(eng, nq, n, k):
     assert i64.dtype == torch.int64 and torch.equal(i64.cpu(), i.cpu().long()) and torch.equal(v64, v)
 
 
+@pytest.mark.parametrize("nq,n,k", [(4, 30000, 10), (3, 9000, 200), (4, 50000, 64)])
+def test_topk_rows_with_infinite_scores(eng, nq, n, k):
+    """Rows holding -inf and +inf scores, one with fewer than k finite ones, go
+    through the selects' histogram cuts (whose score span is then infinite):
+    the result is still the stable sort, -inf ties in column order."""
+    say(f"topk_rows infinite nq={nq} n={n} k={k}")
+    g = torch.Generator().manual_seed(7 * n + k)
+    s = torch.randint(-500, 500, (nq, n), generator=g).float() / 64
+    s[0, ::3] = -float("inf")
+    s[1, : n - k // 2] = -float("inf")  # only k/2 finite scores
+    s[2, ::1000] = float("inf")
+    s[3 % nq, 5::7] = -float("inf")
+    v, i = eng.topk_rows(s.cuda(), k)
+    torch.cuda.synchronize()
+    sn = s.numpy()
+    order = np.lexsort((np.broadcast_to(np.arange(n), sn.shape), -sn), axis=1)[:, :k]
+    np.testing.assert_array_equal(i.cpu().numpy(), order)
+    np.testing.assert_array_equal(v.cpu().numpy(), np.take_along_axis(sn, order, axis=1))
+
+
 def test_topk_rows_errors(eng):
     s = torch.zeros(2, 100, device="cuda")
     with pytest.raises(RuntimeError, match="1 <= k <= 1024"):
