@@ -4,12 +4,15 @@
 
 Objects go to cuda-vector-search_amd/_build/, the library to
 cuda-vector-search_amd/cuda_vector_search/libcvs_hip.so, next to the Python
-package that loads it.  Always rebuilds (the build check must compile).
+package that loads it, with the sha256 of its sources in libcvs_hip.srchash
+(cuda_vector_search._ext.load() rebuilds when the tree no longer matches it).
+Always rebuilds (the build check must compile).
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import os
 import shutil
 import subprocess
@@ -23,6 +26,7 @@ CSRC = PKG_ROOT / "csrc"
 INCLUDE = REPO / "include"
 BUILD = PKG_ROOT / "_build"
 LIB = PKG_ROOT / "cuda_vector_search" / "libcvs_hip.so"
+HASH = LIB.with_name("libcvs_hip.srchash")  # source hash of the library built last
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -53,7 +57,18 @@ def _run(cmd, verbose):
     return r
 
 
+def source_hash() -> str:
+    """sha256 over the sources the library is built from (same rule as
+    cuda_vector_search._ext.source_hash, which load() compares with HASH)."""
+    csrc = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.h")))
+    h = hashlib.sha256()
+    for f in csrc + [INCLUDE / "cvs.h", Path(__file__).resolve()]:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    digest = source_hash()  # of the sources as they are when compilation starts
     BUILD.mkdir(exist_ok=True)
     objs = []
     cmds = []
@@ -66,6 +81,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB)
+    HASH.write_text(digest + "\n")
     return LIB
 
 

@@ -87,7 +87,7 @@ struct DeviceGuard {
 
 int check_inputs(const void* q, const void* x, int64_t nq, int64_t n, int64_t d) {
   if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
-  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (d >= INT_MAX / 2) return fail(CVS_ERR_INVALID, "width %lld is too large", (long long)d);
   if (n < 0 || n >= INT_MAX) return fail(CVS_ERR_INVALID, "corpus must have fewer than 2^31 rows");
   if (nq < 0 || nq >= INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
   if (nq > 0 && (q == nullptr || reinterpret_cast<uintptr_t>(q) % 16 != 0))
@@ -96,6 +96,9 @@ int check_inputs(const void* q, const void* x, int64_t nq, int64_t n, int64_t d)
     return fail(CVS_ERR_INVALID, "corpus must be 16-byte aligned");
   return CVS_OK;
 }
+
+// Widest row whose query fragments the scan holds in registers.
+constexpr int64_t kRegWidth = 1536;
 
 int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
 
@@ -106,8 +109,20 @@ int ks_bucket(int64_t d) { return d <= 384 ? 12 : d <= 768 ? 24 : 48; }
 // one wave's candidate epilogue and barrier waits overlap the other's MFMAs
 // (measured 7% faster than 4 waves of 64 queries).  The auto plan uses it at
 // d = 384 only: narrower rows run the runtime-width kernel, which spills at 256
-// registers per wave and is ~2x slower than two groups of 128 queries.
+// registers per wave and is ~2x slower than two groups of 128 queries.  Rows
+// wider than kRegWidth take the ksmax = 0 kernels: both MFMA operands come from
+// LDS, the queries riding in every stage beside the corpus rows, so any width
+// that is a multiple of 64 works (bq <= 128).
 bool cfg_for(int64_t bq, int64_t d, ScanCfg* c) {
+  if (d > kRegWidth) {
+    switch (bq) {
+      case 16: *c = {16, 1, 1, 1, 0}; return true;
+      case 32: *c = {32, 1, 1, 1, 0}; return true;
+      case 64: *c = {32, 2, 1, 1, 0}; return true;
+      case 128: *c = {32, 4, 1, 2, 0}; return true;
+      default: return false;
+    }
+  }
   switch (bq) {
     case 16:
       *c = {16, 1, 1, 1, ks_bucket(d)};
@@ -295,7 +310,7 @@ int cvs_fused_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int6
   int rc = dev_info(device, &di);
   if (rc != CVS_OK) return rc;
   if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
-  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (d >= INT_MAX / 2) return fail(CVS_ERR_INVALID, "width %lld is too large", (long long)d);
   Plan P;
   rc = make_plan(nq, n, d, k, bq, chunks, flags, di.cus, &P);
   if (rc != CVS_OK) return rc;
@@ -370,7 +385,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       pg.nsample = (int)P.nsample;
       pg.upb = P.upb;
       pg.units = (int)P.units;
-      e = launch_gemv(ks_bucket(d) * 32, pg, (int)ceil_div(P.nsample, 4), s);
+      e = launch_gemv(pg, (int)ceil_div(P.nsample, 4), s);
       if (e != hipSuccess) return hip_fail(e, "gemv sample pass launch");
       SelectArgs sa{};
       sa.lv = umax;
@@ -392,7 +407,7 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
     g.li = li;
     g.lcount = cnt;
     g.nlists = (int)P.nlists;
-    e = launch_gemv(ks_bucket(d) * 32, g, (int)P.gemv_grid, s);
+    e = launch_gemv(g, (int)P.gemv_grid, s);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     mark(3);
   } else {
@@ -663,9 +678,9 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
   int rc = dev_info(device, &di);
   if (rc != CVS_OK) return rc;
   if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
-  if (d < 1 || d > 1536) return fail(CVS_ERR_INVALID, "row width %lld must be in [1, 1536]", (long long)d);
-  if (dst_width < d || dst_width > 1536)
-    return fail(CVS_ERR_INVALID, "destination width %lld must be in [d, 1536]", (long long)dst_width);
+  if (d < 1 || d >= INT_MAX) return fail(CVS_ERR_INVALID, "row width %lld must be in [1, 2^31)", (long long)d);
+  if (dst_width < d || dst_width >= INT_MAX)
+    return fail(CVS_ERR_INVALID, "destination width %lld must be in [d, 2^31)", (long long)dst_width);
   if (src_stride < d) return fail(CVS_ERR_INVALID, "source row stride must be >= d");
   if (n < 0) return fail(CVS_ERR_INVALID, "row count must be >= 0");
   if (n == 0) return CVS_OK;
@@ -700,6 +715,9 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
 namespace {
 
 constexpr int64_t kQ8SampleDiv = 8;
+// Widest fp16 row the int8 companion covers (int8 rows of 384, 768 or 1536
+// bytes; wider corpora are searched by the fp16 scan).
+constexpr int64_t kQ8MaxWidth = 1536;
 
 // From this batch size on, the select rescores the candidates itself (one
 // workgroup per query, the k of largest bound first, then only those that can
@@ -739,6 +757,9 @@ struct Q8Plan {
 };
 
 int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus, Q8Plan* out) {
+  if (d > kQ8MaxWidth)
+    return fail(CVS_ERR_INVALID, "the int8 pre-filter supports widths up to %lld, not %lld", (long long)kQ8MaxWidth,
+                (long long)d);
   Q8Plan P;
   int rc = make_plan(nq, n, d, k, 0, 0, flags, cus, &P.sample, kQ8SampleDiv);
   if (rc != CVS_OK) return rc;
@@ -879,7 +900,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       pg.nsample = (int)S.nsample;
       pg.upb = S.upb;
       pg.units = (int)S.units;
-      e = launch_gemv(ks_bucket(d) * 32, pg, (int)ceil_div(S.nsample, 4), s);
+      e = launch_gemv(pg, (int)ceil_div(S.nsample, 4), s);
     } else {
       ScanArgs pa{};
       pa.q = qh;
@@ -942,7 +963,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     g.qmeta = qm;
     g.bmeta = bmeta;
     g.gamma = gamma;
-    e = launch_gemv(1536, g, (int)P.gemv_grid, s);
+    e = launch_gemv(g, (int)P.gemv_grid, s);
     if (e != hipSuccess) return hip_fail(e, "int8 gemv launch");
   } else {
     ScanArgs a{};
@@ -1021,7 +1042,9 @@ extern "C" {
 int cvs_q8_corpus_bytes(int64_t n, int64_t d, int64_t* bytes) {
   if (bytes == nullptr) return fail(CVS_ERR_INVALID, "bytes must not be null");
   if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
-  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (d > kQ8MaxWidth)
+    return fail(CVS_ERR_INVALID, "the int8 pre-filter supports widths up to %lld, not %lld", (long long)kQ8MaxWidth,
+                (long long)d);
   if (n < 1 || n >= INT_MAX) return fail(CVS_ERR_INVALID, "corpus must have between 1 and 2^31-1 rows");
   *bytes = q8_layout(n, d).bytes;
   return CVS_OK;
@@ -1057,7 +1080,9 @@ int cvs_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int devi
   int rc = dev_info(device, &di);
   if (rc != CVS_OK) return rc;
   if (d <= 0 || d % 64 != 0) return fail(CVS_ERR_INVALID, "width must be a multiple of 64 (zero-pad it)");
-  if (d > 1536) return fail(CVS_ERR_INVALID, "width %lld exceeds the 1536 supported by the gfx950 kernels", (long long)d);
+  if (d > kQ8MaxWidth)
+    return fail(CVS_ERR_INVALID, "the int8 pre-filter supports widths up to %lld, not %lld", (long long)kQ8MaxWidth,
+                (long long)d);
   Q8Plan P;
   rc = make_q8_plan(nq, n, d, k, flags, di.cus, &P);
   if (rc != CVS_OK) return rc;

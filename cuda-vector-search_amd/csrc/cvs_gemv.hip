@@ -44,6 +44,11 @@ __device__ __forceinline__ float dot8(half8 a, half8 b, float acc) {
 }
 
 // PMAX = max 128-byte pieces per row handled by one lane (d <= 64*PMAX).
+// PMAX = 0: rows of any width, taken kWide pieces at a time; the query's pieces
+// are re-read per row group (a wave's 8 row groups read the same 128 bytes per
+// load, and the whole query stays in the vector L1 / L2).
+constexpr int kWide = 8;
+
 template <int PMAX, int MODE>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
   constexpr bool Q8 = (MODE == kAppendQ8);
@@ -63,7 +68,9 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
 
   // Unconditional loads (a piece past d re-reads the last one and is never
   // used): a per-load branch would put each behind a wait for the previous one.
-  half8 qv[PMAX];
+  constexpr bool WIDE = (PMAX == 0);
+  static_assert(!WIDE || !Q8, "the int8 companion holds rows of at most 1536 bytes");
+  half8 qv[WIDE ? 1 : PMAX];
 #pragma unroll
   for (int p = 0; p < PMAX; ++p) qv[p] = *(const half8*)(qb + min(p, np - 1) * 128 + sub * 16);
   float4 qm = float4{0.f, 0.f, 0.f, 0.f};
@@ -92,15 +99,38 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
   }
 
   for (int64_t r0 = r_begin; r0 < r_end; r0 += 8 * kUnr) {
-    half8 xv[kUnr][PMAX];
+    half8 xv[kUnr][WIDE ? 1 : PMAX];
+    const unsigned char* srcs[kUnr];
 #pragma unroll
     for (int u = 0; u < kUnr; ++u) {
       int64_t row = r0 + u * 8 + rg;
       if (row >= n) row = n - 1;
-      const unsigned char* src = xb + row * rb + sub * 16;
+      srcs[u] = xb + row * rb + sub * 16;
 #pragma unroll
       for (int p = 0; p < PMAX; ++p)
-        if (p < np) xv[u][p] = __builtin_nontemporal_load((const half8*)(src + p * 128));
+        if (p < np) xv[u][p] = __builtin_nontemporal_load((const half8*)(srcs[u] + p * 128));
+    }
+    // WIDE: this lane's partial dot products, kWide pieces at a time
+    float wacc[kUnr];
+#pragma unroll
+    for (int u = 0; u < kUnr; ++u) wacc[u] = 0.f;
+    if constexpr (WIDE) {
+#pragma unroll 1
+      for (int p0 = 0; p0 < np; p0 += kWide) {
+        half8 qw[kWide], xw[kUnr][kWide];
+#pragma unroll
+        for (int p = 0; p < kWide; ++p) {
+          const int pp = min(p0 + p, np - 1);  // past the row: re-read the last piece, unused
+          qw[p] = *(const half8*)(qb + pp * 128 + sub * 16);
+#pragma unroll
+          for (int u = 0; u < kUnr; ++u) xw[u][p] = __builtin_nontemporal_load((const half8*)(srcs[u] + pp * 128));
+        }
+#pragma unroll
+        for (int p = 0; p < kWide; ++p)
+          if (p0 + p < np)
+#pragma unroll
+            for (int u = 0; u < kUnr; ++u) wacc[u] = dot8(xw[u][p], qw[p], wacc[u]);
+      }
     }
     // kAppendQ8: the 16 rows of this iteration lie in one 64-row block
     // (per-wave ranges start at multiples of 16); its meta comes through the
@@ -127,6 +157,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
         ia += __shfl_xor(ia, 4);
         acc = fmaf((float)ia, cq, slack);  // upper bound of the exact score
       } else {
+        if (WIDE) acc = wacc[u];
 #pragma unroll
         for (int p = 0; p < PMAX; ++p)
           if (p < np) acc = dot8(xv[u][p], qv[p], acc);
@@ -203,7 +234,7 @@ hipError_t launch_q8(const GemvArgs& a, int grid, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s) {
+hipError_t launch_gemv(const GemvArgs& a, int grid, hipStream_t s) {
   if (a.mode == kAppendQ8) {  // d = int8 row bytes
     if (a.qmeta == nullptr || a.bmeta == nullptr || a.rows_per_wave % 16 != 0) return hipErrorInvalidValue;
     if (a.d == 384) return launch_q8<3>(a, grid, s);
@@ -211,11 +242,11 @@ hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s) {
     if (a.d == 1536) return launch_q8<12>(a, grid, s);
     return hipErrorInvalidValue;
   }
-  if (a.d > dmax) return hipErrorInvalidValue;
-  if (dmax <= 384) return launch_p<6>(a, grid, s);
-  if (dmax <= 768) return launch_p<12>(a, grid, s);
-  if (dmax <= 1536) return launch_p<24>(a, grid, s);
-  return hipErrorInvalidValue;
+  if (a.d <= 0 || a.d % 64 != 0) return hipErrorInvalidValue;
+  if (a.d <= 384) return launch_p<6>(a, grid, s);
+  if (a.d <= 768) return launch_p<12>(a, grid, s);
+  if (a.d <= 1536) return launch_p<24>(a, grid, s);
+  return launch_p<0>(a, grid, s);
 }
 
 }  // namespace cvs

@@ -161,7 +161,8 @@ struct Q8QueryArgs {
 };
 
 // Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,
-// tile rows = rs*rb*ms, widest row = ksmax * (ms == 16 ? 32 : 16).
+// tile rows = rs*rb*ms, widest row = ksmax * (ms == 16 ? 32 : 16); ksmax = 0:
+// rows of any width (queries staged through LDS instead of held in registers).
 // Row splits of a scan configuration (waves = qs * rs): 4 waves, one per SIMD,
 // except 8 (two per SIMD) for qs = 8.
 constexpr int scan_row_splits(int qs) { return qs >= 4 ? 1 : 4 / qs; }
@@ -173,13 +174,13 @@ struct ScanCfg {
   int rs() const { return scan_row_splits(qs); }
   int tile_rows() const { return rs() * rb * ms; }
   int wave_rows() const { return rb * ms; }
-  int dmax() const { return ksmax * (ms == 16 ? 32 : 16); }
+  int dmax() const { return ksmax * (ms == 16 ? 32 : 16); }  // 0: no limit
   int units_per_tile() const { return rs() * (64 / ms); }
 };
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
-hipError_t launch_gemv(int dmax, const GemvArgs& a, int grid, hipStream_t s);
+hipError_t launch_gemv(const GemvArgs& a, int grid, hipStream_t s);  // any d % 64 == 0 (int8: 384/768/1536 bytes)
 hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);  // 0 final, 1 threshold, 2 rescore
 hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, hipStream_t s);

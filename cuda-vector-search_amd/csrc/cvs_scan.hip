@@ -121,9 +121,17 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int TR = RS * RW;        // tile rows
   constexpr int KPS = 64 / M::KSZ;   // MFMA k-steps per 64-column stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
-  constexpr int FPS = TRB * KPS;     // 1 KB DMA loads (8 rows x 128 bytes) per stage
+  constexpr int FC = TRB * KPS;      // 1 KB DMA loads (8 rows x 128 bytes) of corpus rows per stage
+  static_assert(FC * 8 == TR, "a stage load covers 8 rows of 128 bytes");
+  // QL (KSMAX == 0, rows of any width): the queries are not held in registers
+  // but ride in every stage beside the corpus rows, QA rows of 128 bytes (the
+  // query block padded so every wave issues the same number of loads), and the
+  // MFMAs read both operands from LDS.
+  constexpr bool QL = (KSMAX == 0);
+  constexpr int QA = QL ? ((BQ + 8 * NW - 1) / (8 * NW)) * (8 * NW) : 0;
+  constexpr int FPS = FC + QA / 8;   // 1 KB DMA loads per stage
   static_assert(FPS % NW == 0, "every wave must issue the same number of stage loads");
-  static_assert(FPS * 8 == TR, "a stage load covers 8 rows of 128 bytes");
+  static_assert(!QL || (!FULLW && MODE != kAppendQ8), "queries in LDS: fp16 rows of a runtime width");
   constexpr int LPW = FPS / NW;      // stage loads per wave
   constexpr int STAGE = FPS * 1024;
   constexpr int NBUF = ((QS >= 4 ? 56 : 40) * 1024) / STAGE + 2;
@@ -206,13 +214,22 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   const _Float16* src[LPW];
   int64_t src_row[LPW];
   int poff[LPW];  // this lane's 16-byte piece of its row, in halfs
+  bool qload[LPW];  // QL: this (wave-uniform) load fetches query rows, the same every tile
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int f = w + NW * j;
-    const int rl = f * 8 + (lane >> 3);  // tile row of this lane's load
-    poff[j] = ((lane & 7) ^ piece_swz(rl)) * 8;
-    src_row[j] = t_begin * TR + rl;
-    src[j] = a.x + src_row[j] * d + poff[j];
+    qload[j] = QL && f >= FC;
+    if (qload[j]) {  // query-area row ql: query grp*BQ + ql (padding rows re-read the last query)
+      const int ql = (f - FC) * 8 + (lane >> 3);
+      poff[j] = ((lane & 7) ^ piece_swz(ql)) * 8;
+      src_row[j] = -1;  // never clamped
+      src[j] = a.q + (int64_t)min(grp * BQ + ql, a.nq - 1) * d + poff[j];
+    } else {
+      const int rl = f * 8 + (lane >> 3);  // tile row of this lane's load
+      poff[j] = ((lane & 7) ^ piece_swz(rl)) * 8;
+      src_row[j] = t_begin * TR + rl;
+      src[j] = a.x + src_row[j] * d + poff[j];
+    }
   }
   auto issue_next = [&]() {
     unsigned char* buf = smem + it_buf * STAGE;
@@ -229,8 +246,10 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       ++it_t;
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        src[j] += (int64_t)TR * d;
-        src_row[j] += TR;
+        if (!qload[j]) {
+          src[j] += (int64_t)TR * d;
+          src_row[j] += TR;
+        }
       }
     }
     if (++it_buf == NBUF) it_buf = 0;
@@ -244,8 +263,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // each behind a wait for the previous one): a column past nq loads query
   // nq-1 (its scores are never reported: its threshold is +inf and kMax skips
   // it), a k-step past d loads the last one (the stage loop never uses it).
-  half8 qf[QB][KSMAX];
-  {
+  half8 qf[QB][QL ? 1 : KSMAX];
+  if constexpr (!QL) {
     half8 ld[QB][KSMAX];
     const int ksl = d / M::KSZ - 1;
 #pragma unroll
@@ -386,6 +405,20 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       for (int rb = 0; rb < RB; ++rb)
         f[kk][rb] = *(const half8*)(buf + aoff[kk] + rb * MS * 128);
   };
+  // QL: B fragment of k-step kk, query block qb: query-area row
+  // Rq = qs*QW + qb*MS + col (after the TR corpus rows), same piece rule.
+  // (Unused, and dropped by the compiler, when the queries sit in registers.)
+  int boff[KPS];
+#pragma unroll
+  for (int kk = 0; kk < KPS; ++kk)
+    boff[kk] = (TR + qs * QW + col) * 128 + (((kk * G + kg) ^ piece_swz(col)) << 4);
+  auto read_qstage = [&](int buf_idx, half8 (&f)[KPS][QB]) {
+    const unsigned char* buf = smem + buf_idx * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) f[kk][qb] = *(const half8*)(buf + boff[kk] + qb * MS * 128);
+  };
   // 8-wave full-width tiles (256 registers per wave) read the A fragments of
   // one k-step LA k-steps ahead into a ring of SL = LA + 1 slots (slot g % SL
   // holds k-step g) instead of a whole stage ahead: 24 instead of 64 VGPRs of
@@ -397,6 +430,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int LA = 2, SL = LA + 1;
   constexpr bool KRING = FULLW && NW == 8 && (KT % SL == 0);
   half8 ab[KRING ? 1 : 2][KPS][RB];  // stage s in ab[s & 1] (static within a tile), stage s+1 prefetched
+  half8 bb[QL ? 2 : 1][KPS][QB];     // QL: the queries' B fragments, staged like ab
   half8 fr[KRING ? SL : 1][RB];
   auto read_ks = [&](int buf_idx, int kk, half8 (&f)[RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
@@ -410,8 +444,29 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     for (int g = 0; g < LA; ++g) read_ks(0, g, fr[g]);
   } else {
     read_stage(0, ab[0]);
+    if constexpr (QL) read_qstage(0, bb[0]);
   }
   int cur_buf = 0;
+  // QL: one stage of a runtime-length tile.  Same sync as the register-query
+  // kernels: wait until the next stage has landed for every wave (the barrier
+  // also retires every read of the buffer issue_next() refills), read its A
+  // and B fragments, then run this stage's MFMAs on the ones read before.
+  auto ql_stage = [&](half8 (&ca)[KPS][RB], half8 (&cb)[KPS][QB], half8 (&na)[KPS][RB],
+                      half8 (&nb)[KPS][QB], auto& acc) {
+    wait_vmcnt_lgkm0<(NBUF - 3) * LPW>();
+    __builtin_amdgcn_s_barrier();
+    issue_next();
+    const int nxt = (cur_buf + 1 == NBUF) ? 0 : cur_buf + 1;
+    read_stage(nxt, na);
+    read_qstage(nxt, nb);
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) acc[qb][rb] = M::run(ca[kk][rb], cb[kk][qb], acc[qb][rb]);
+    cur_buf = nxt;
+  };
 
   for (int64_t t = t_begin; t < t_end; ++t) {
     acc_t acc[QB][RB];
@@ -474,7 +529,24 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
         cur_buf = nxt;
       }
     }
-    if (!KRING && (nc & 1)) {  // the next tile's first stage sits in ab[1]
+    if constexpr (QL) {
+      // stages in pairs, so that the fragment buffers are indexed statically
+#pragma unroll 1
+      for (int c = 0; c < nc; c += 2) {
+        ql_stage(ab[0], bb[0], ab[1], bb[1], acc);
+        if (c + 1 < nc) ql_stage(ab[1], bb[1], ab[0], bb[0], acc);
+      }
+      if (nc & 1) {  // the next tile's first stage sits in ab[1] / bb[1]
+#pragma unroll
+        for (int kk = 0; kk < KPS; ++kk) {
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) ab[0][kk][rb] = ab[1][kk][rb];
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) bb[0][kk][qb] = bb[1][kk][qb];
+        }
+      }
+    }
+    if (!QL && !KRING && (nc & 1)) {  // the next tile's first stage sits in ab[1]
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
@@ -669,33 +741,35 @@ hipError_t launch_one_q8(const ScanArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+// One mode of one configuration: the full-width kernel when the row width is
+// exactly KS k-steps, else the runtime-width one (the only one for KS = 0).
+template <int MS, int QS, int QB, int RB, int KS, int MODE>
+void launch_mode(bool full, const ScanArgs& a, int grid, hipStream_t s) {
+  if constexpr (KS > 0) {
+    if (full) {
+      hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, MODE, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, MODE, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+}
+
 template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
-  const bool full = (a.d == KS * Mfma<MS>::KSZ);
+  const bool full = KS > 0 && (a.d == KS * Mfma<MS>::KSZ);
+  if (KS > 0 && a.d > KS * Mfma<MS>::KSZ) return hipErrorInvalidValue;
   switch (mode) {
     case kAppend:
-      if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppend, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+      launch_mode<MS, QS, QB, RB, KS, kAppend>(full, a, grid, s);
       break;
     case kMax:
-      if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMax, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+      launch_mode<MS, QS, QB, RB, KS, kMax>(full, a, grid, s);
       break;
     case kStoreF32:
-      if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF32, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+      launch_mode<MS, QS, QB, RB, KS, kStoreF32>(full, a, grid, s);
       break;
     case kStoreF16:
-      if (full)
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kStoreF16, false>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+      launch_mode<MS, QS, QB, RB, KS, kStoreF16>(full, a, grid, s);
       break;
     default:
       return hipErrorInvalidValue;
@@ -704,7 +778,9 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
 }
 
 // The instantiated configurations: (MS, QS, QB, RB, KSMAX).  KSMAX * KSZ is the
-// widest row each one accepts (KSZ = 32 for MS = 16, 16 for MS = 32).
+// widest row each one accepts (KSZ = 32 for MS = 16, 16 for MS = 32); KSMAX = 0
+// takes rows of any width (multiple of 64), with the queries staged through LDS
+// beside the corpus rows instead of held in registers.
 #define CVS_SCAN_CONFIGS(X) \
   X(16, 1, 1, 1, 12)        \
   X(16, 1, 1, 1, 24)        \
@@ -717,7 +793,11 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   X(32, 2, 1, 1, 48)        \
   X(32, 4, 1, 2, 24)        \
   X(32, 4, 1, 2, 48)        \
-  X(32, 8, 1, 2, 24)
+  X(32, 8, 1, 2, 24)        \
+  X(16, 1, 1, 1, 0)         \
+  X(32, 1, 1, 1, 0)         \
+  X(32, 2, 1, 1, 0)         \
+  X(32, 4, 1, 2, 0)
 
 // int8 pre-filter configurations (KS in 32-byte k-steps: 12, 24, 48 = int8 rows
 // of 384, 768, 1536 bytes).

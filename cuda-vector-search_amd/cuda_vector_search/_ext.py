@@ -10,21 +10,34 @@ object with the reference extension's methods
 with the reference's argument checks and ``RuntimeError`` messages
 (kernels.cu:451-470).  Underneath, torch only supplies device memory and the
 current stream; every score and every selection is computed by the HIP
-kernels.  There is no fallback inside this module: if the library cannot be
-loaded on a GPU that ``available()`` accepts, ``load()`` raises.
+kernels.  There is no fallback inside this module: ``load()`` raises when the
+library cannot be loaded, and ``available()`` (which ``Index`` consults, as the
+reference's does at index.py:78) then returns False with a warning that carries
+the cause, so an ``Index`` takes the reference's own torch path instead.
+
+Stale binaries: ``build()`` records a hash of the sources it compiled
+(``csrc/``, ``include/cvs.h``, ``build.py``) beside the library, and ``load()``
+rebuilds when the tree's sources no longer match it, as torch's JIT extensions
+(the reference's ``_ext.py:29-46``) rebuild on a source change.
 """
 
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import threading
+import warnings
 from pathlib import Path
 
 _lock = threading.Lock()
 _mod = None
+_load_error: str | None = None
 
 LIBRARY = Path(__file__).with_name("libcvs_hip.so")
+HASH_FILE = Path(__file__).with_name("libcvs_hip.srchash")
 ARCH = "gfx950"
+_PKG_ROOT = Path(__file__).resolve().parent.parent
+_REPO = _PKG_ROOT.parent
 
 # Flags of cvs_fused_topk (include/cvs.h).
 FLAG_NO_PREPASS = 1
@@ -33,7 +46,7 @@ FLAG_NO_GEMV = 4
 FLAG_IDS_INT64 = 8  # ids as int64 (Index.search's dtype) instead of the reference's int32
 
 
-def available() -> bool:
+def device_supported() -> bool:
     """True when the current torch device is an MI355X-class (gfx950) GPU."""
     import torch
 
@@ -44,6 +57,57 @@ def available() -> bool:
     except Exception:  # pragma: no cover - exotic torch builds
         return False
     return str(arch).split(":")[0] == ARCH
+
+
+def available() -> bool:
+    """True when the engine can run here: a gfx950 GPU and a library that loads.
+
+    Replaces ``_ext.py:15-21`` of the reference.  A load failure is reported once
+    as a ``RuntimeWarning`` (with its cause) and makes this False."""
+    if not device_supported():
+        return False
+    try:
+        load()
+        return True
+    except Exception as e:  # noqa: BLE001 - any failure means "not available"
+        global _load_error
+        if _load_error is None:
+            _load_error = str(e)
+            warnings.warn(f"libcvs_hip could not be loaded; searches use the torch path: {e}",
+                          RuntimeWarning, stacklevel=2)
+        return False
+
+
+def source_files() -> list[Path]:
+    """The files whose contents the built library depends on."""
+    csrc = _PKG_ROOT / "csrc"
+    files = sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.h")))
+    return files + [_REPO / "include" / "cvs.h", _PKG_ROOT / "build.py"]
+
+
+def source_hash() -> str | None:
+    """sha256 over the library's sources (None when they are not in this tree)."""
+    files = source_files()
+    if not all(f.exists() for f in files):
+        return None
+    h = hashlib.sha256()
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
+def built_hash() -> str | None:
+    """The source hash recorded when the library was built (None if unknown)."""
+    try:
+        return HASH_FILE.read_text().strip() or None
+    except OSError:
+        return None
+
+
+def is_current() -> bool:
+    """Whether the library exists and was built from the sources in this tree."""
+    want = source_hash()
+    return LIBRARY.exists() and (want is None or built_hash() == want)
 
 
 def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -337,27 +401,27 @@ class Engine:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile libcvs_hip.so in-tree (hipcc, gfx950)."""
+    """Compile libcvs_hip.so in-tree (hipcc, gfx950) and record its source hash."""
     import importlib.util
 
-    spec = importlib.util.spec_from_file_location(
-        "_cvs_build", Path(__file__).resolve().parent.parent / "build.py")
+    spec = importlib.util.spec_from_file_location("_cvs_build", _PKG_ROOT / "build.py")
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     return mod.build(verbose=verbose)
 
 
 def load(verbose: bool = False) -> Engine:
-    """Load (building once if the library is missing) and return the engine."""
+    """Load (building first if the library is missing or older than its sources)
+    and return the engine."""
     global _mod
     if _mod is not None:
         return _mod
     with _lock:
         if _mod is not None:
             return _mod
-        if not available():
+        if not device_supported():
             raise RuntimeError("cuda-vector-search kernels need an AMD Instinct MI355X (gfx950) GPU")
-        if not LIBRARY.exists():
+        if not is_current():
             build(verbose)
         lib = open_library()
         import torch

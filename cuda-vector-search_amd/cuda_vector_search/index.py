@@ -11,6 +11,7 @@ messages, ``.npy`` + ``<path>.json`` persistence).  The difference is underneath
 from __future__ import annotations
 
 import json
+import threading
 from pathlib import Path
 
 import numpy as np
@@ -23,7 +24,7 @@ PAD = 64            # widths are zero-padded to a multiple of this (the MFMA dep
 MAX_FUSED_K = 256   # largest k of the fused path
 MAX_EXACT_K = 1024  # largest k of the exact large-k path (score matrix + row top-k)
 _SCORE_BLOCK_BYTES = 1 << 31  # fp32 score rows computed per block on the large-k path
-MAX_KERNEL_WIDTH = 1536  # widest (padded) rows the gfx950 kernels accept
+Q8_MAX_WIDTH = 1536  # widest (padded) rows the int8 companion covers; wider corpora use the fp16 scan
 _NORM_CHUNK = 1 << 18
 # int8 pre-filter (an int8 companion of the corpus scanned instead of the fp16
 # rows; exact results).  Built by default for corpora of at least Q8_MIN_ROWS
@@ -48,7 +49,7 @@ METHODS = ("auto", "fused", "twopass", "torch", "int8")
 
 def int8_builds(n: int, width: int) -> bool:
     """Whether Index builds the int8 companion by default (int8_prefilter=None)."""
-    return n >= Q8_MIN_ROWS and Q8_MIN_WIDTH < width <= MAX_KERNEL_WIDTH
+    return n >= Q8_MIN_ROWS and Q8_MIN_WIDTH < width <= Q8_MAX_WIDTH
 
 
 def _int8_faster(n: int, nq: int, k: int) -> bool:
@@ -99,9 +100,15 @@ class Index:
             without a copy (and normalised in place for cosine).
         int8_prefilter: build the int8 companion used by ``method="int8"`` (and by
             "auto" where it is faster): None = when the corpus is large enough
-            (>= 2^18 rows wider than 256), True = always on a gfx950 GPU, False =
-            never.  It holds one byte per stored element, built once here; like
-            the normalisation, it reflects the corpus at construction.
+            (>= 2^18 rows, padded width in (256, 1536]), True = always on a gfx950
+            GPU (widths up to 1536), False = never.  It costs one byte per stored
+            element plus 16 bytes per 64 rows (``int8_bytes``): +50% of the fp16
+            corpus's HBM (1M x 768: +768 MB).  It is built here and rebuilt before
+            the next int8 search whenever the stored rows have changed through
+            torch (in-place ops on ``_x``, ``embeddings`` or, with ``copy=False``,
+            the caller's tensor bump its version counter).  Writes that bypass
+            torch (raw pointers, other libraries) are not seen: call
+            ``refresh_int8()`` after them.
     """
 
     def __init__(self, embeddings, metric: str = "cosine", device=None, copy: bool = True,
@@ -123,27 +130,73 @@ class Index:
         if copy and x.data_ptr() == src.data_ptr():  # .to() returned the caller's storage
             x = x.clone()
         x = x.contiguous()
+        # The reference asks only _ext.available() here (index.py:78); available()
+        # is False when the engine library cannot be loaded, and then the index
+        # uses the torch path as the reference does without its kernels.
         self._use_kernels = on_gpu and _ext.available()
-        if self._use_kernels and x.shape[1] <= MAX_KERNEL_WIDTH:
+        if self._use_kernels:
             # one HIP pass each: normalise in place (the caller's tensor too when
             # copy=False, as in the reference), then zero-pad into a new tensor
             eng = _ext.load()
             if metric == "cosine" and x.shape[0] > 0:
                 eng.prep_rows(x, x, True)
             width = x.shape[1] + (-x.shape[1]) % PAD
-            if width != x.shape[1] and width <= MAX_KERNEL_WIDTH:
+            if width != x.shape[1]:
                 xp = torch.empty((x.shape[0], width), dtype=x.dtype, device=x.device)
                 eng.prep_rows(x, xp, False)
                 x = xp
-            self._x = _padded(x)
+            self._x = x
         else:
             if metric == "cosine":
                 _normalize_(x)
             self._x = _padded(x) if on_gpu else x
         self._xq = None
-        if self._use_kernels and self._x.shape[1] <= MAX_KERNEL_WIDTH and int8_prefilter is not False:
+        self._xq_stamp = None  # (version, data_ptr, shape) of _x when _xq was built
+        self._xq_ready = None  # event recorded after the build of _xq
+        self._xq_lock = threading.Lock()
+        if self._use_kernels and int8_prefilter is not False and self._x.shape[1] <= Q8_MAX_WIDTH:
             if int8_prefilter or int8_builds(self._x.shape[0], self._x.shape[1]):
-                self._xq = _ext.load().q8_build(self._x)
+                self._build_int8()
+
+    def _corpus_stamp(self):
+        return (self._x._version, self._x.data_ptr(), tuple(self._x.shape))
+
+    def _build_int8(self) -> None:
+        stamp = self._corpus_stamp()
+        xq = _ext.load().q8_build(self._x)  # enqueued on the current stream
+        ready = torch.cuda.Event()
+        ready.record()
+        self._xq, self._xq_stamp, self._xq_ready = xq, stamp, ready
+
+    def _int8_companion(self, build: bool):
+        """The int8 companion, current with the stored rows: rebuilt when they
+        changed since it was built (and built when ``build`` and there is none).
+        Thread-safe, and safe across streams: the caller's stream waits for the
+        build, and the companion's memory is held for that stream's work even if
+        another thread replaces it meanwhile.  None when there is none and
+        ``build`` is False."""
+        with self._xq_lock:
+            if self._xq is None and not build:
+                return None
+            if self._xq is None or self._xq_stamp != self._corpus_stamp():
+                self._build_int8()
+            xq, ready = self._xq, self._xq_ready
+        stream = torch.cuda.current_stream(self.device)
+        stream.wait_event(ready)
+        xq.record_stream(stream)
+        return xq
+
+    def refresh_int8(self) -> None:
+        """Rebuild the int8 companion from the stored rows (after writes torch did not see)."""
+        with self._xq_lock:
+            if self._xq is not None:
+                self._build_int8()
+
+    @property
+    def int8_bytes(self) -> int:
+        """Device bytes held by the int8 companion (0 when there is none)."""
+        xq = self._xq
+        return 0 if xq is None else int(xq.numel())
 
     # -- basics -------------------------------------------------------------
     def __len__(self) -> int:
@@ -162,7 +215,7 @@ class Index:
             raise ValueError(f"queries must be [b, {self.dim}]")
         q = q.to(self.device, self._x.dtype).contiguous()
         width = self._x.shape[1]
-        if (self._use_kernels and width <= MAX_KERNEL_WIDTH and q.shape[0] > 0
+        if (self._use_kernels and q.shape[0] > 0
                 and (self.metric == "cosine" or width != q.shape[1])):
             # normalise (cosine) + zero-pad in one HIP pass into a new tensor
             out = torch.empty((q.shape[0], width), dtype=q.dtype, device=q.device)
@@ -185,7 +238,9 @@ class Index:
                         (same results as "fused", k <= 256)
             "auto"    - int8 where it is faster (batch 1; over >= 2^19 rows, batches of
                         <= 64 queries or k <= 16), else fused, for k <= 256; exact
-                        fp32 scores + row top-k for k <= 1024; else torch
+                        fp32 scores + row top-k for k <= 1024; else torch.  Any
+                        width: rows wider than 1536 run the fp16 kernels (the int8
+                        companion covers widths up to 1536)
         """
         if method not in METHODS:
             raise ValueError(f"method must be one of {METHODS}")
@@ -195,10 +250,9 @@ class Index:
         k = min(k, len(self))
         q = self._prep_queries(queries)
         if method == "auto":
-            width_ok = self._use_kernels and self._x.shape[1] <= MAX_KERNEL_WIDTH
-            if width_ok and k <= MAX_FUSED_K:
+            if self._use_kernels and k <= MAX_FUSED_K:
                 method = "int8" if self._int8_wins(q.shape[0], k) else "fused"
-            elif width_ok and k <= MAX_EXACT_K:
+            elif self._use_kernels and k <= MAX_EXACT_K:
                 return self._search_large_k(q, k)
             else:
                 method = "torch"
@@ -207,9 +261,10 @@ class Index:
         if method == "int8":
             if k > MAX_FUSED_K:
                 raise ValueError(f"int8 search supports k <= {MAX_FUSED_K}")
-            if self._xq is None:
-                self._xq = _ext.load().q8_build(self._x)
-            v, i, _ = _ext.load().q8_topk(q, self._x, self._xq, k, flags=_ext.FLAG_IDS_INT64)
+            if self._x.shape[1] > Q8_MAX_WIDTH:
+                raise ValueError(f"int8 search supports widths up to {Q8_MAX_WIDTH}")
+            xq = self._int8_companion(build=True)
+            v, i, _ = _ext.load().q8_topk(q, self._x, xq, k, flags=_ext.FLAG_IDS_INT64)
             return v, i
         if method == "fused":
             if k > MAX_FUSED_K:

@@ -14,8 +14,11 @@
  * appear in the signatures.  Conventions shared by every entry point:
  *
  *   - q is [nq, d] and x is [n, d], fp16 (IEEE binary16), row-major,
- *     contiguous, 16-byte aligned, on `device`; d is a multiple of 64 (the
- *     caller zero-pads, as index.py:27-32 does) and at most 1536.
+ *     contiguous, 16-byte aligned, on `device`; d is any multiple of 64 (the
+ *     caller zero-pads, as index.py:27-32 does), as in the reference's
+ *     check_matrix (kernels.cu:451-458).  Rows up to 1536 wide run kernels that
+ *     hold the queries in registers; wider rows stage them through LDS.  The
+ *     int8 pre-filter (cvs_q8_*) covers d <= 1536.
  *   - `stream` is a hipStream_t (NULL = the default stream).  Work is enqueued
  *     asynchronously on it; no entry point synchronises or allocates device
  *     memory.  Results are valid once the stream reaches them.
@@ -143,7 +146,7 @@ int cvs_topk_rows_plan(int64_t nq, int64_t n, int64_t k, int device, int64_t* wo
  * Row preparation, one pass: dst[r, 0:d] = src[r, 0:d], divided by
  * max(||src[r, 0:d]||_2, 1e-12) (fp32 arithmetic, rounded once to fp16) when
  * normalize != 0, and dst[r, d:dst_width] = 0.  Rows are fp16; src rows are
- * src_stride elements apart, dst rows dst_width apart (d <= dst_width <= 1536).
+ * src_stride elements apart, dst rows dst_width apart (d <= dst_width < 2^31).
  * src == dst (in place) is allowed when src_stride == dst_width; other
  * overlaps are not.  Replaces the torch sequences of index.py:35-41
  * (_normalize_) and index.py:27-32 (_pad_width) used for cosine queries on

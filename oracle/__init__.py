@@ -28,6 +28,9 @@ Contents, each restating one reference function (file:line into the reference):
 * ``check_exact``        - the acceptance rule of ``tests/test_search.py:21-44``
   plus the id-parity rule (ids identical except inside the near-tie band of the
   k-th score).
+* ``check_order``        - the same parity position by position: above the band,
+  the ids come in the oracle's order (score desc, id asc, ``kernels.cu:277-279``)
+  except among rows whose scores agree closer than the fp32 sum-order error.
 
 Pinning (see ``tests/test_oracle.py``): fp16 decoding is checked exhaustively
 against numpy; ``topk`` is checked against committed golden vectors made by an
@@ -327,3 +330,28 @@ def check_exact(q, x, k: int, scores_got, ids_got, tol: float = 1e-3, full=None)
             raise ParityError(f"row {r}: a true top-k id outside the near-tie band is missing")
     hit = sum(len(set(a) & set(c)) for a, c in zip(i_got.tolist(), part.tolist()))
     return hit / i_got.size
+
+
+def check_order(v_got, i_got, ov, oi, band: float = 1e-3, eps: float = 1e-5) -> None:
+    """Ids equal the oracle's position by position above the near-tie band of
+    the k-th score (``kernels.cu:277-279`` order), except that rows whose oracle
+    scores lie within ``eps`` of each other (exact duplicates, perturbations
+    closer than the fp32 sum-order error) may come in either order among
+    themselves: each such run of positions must hold the same ids.  A run that
+    reaches into the band belongs to the band (``check_exact`` covers it).
+    ``v_got``/``i_got`` from the engine, ``ov``/``oi`` from ``topk``; [b, k]."""
+    i_got, ov, oi = (np.asarray(a) for a in (i_got, ov, oi))
+    b, k = ov.shape
+    if np.asarray(v_got).shape != (b, k) or i_got.shape != (b, k):
+        raise ParityError("shape mismatch")
+    for r in range(b):
+        m = int((ov[r] > ov[r, -1] + band).sum())  # a prefix: ov is sorted
+        j = 0
+        while j < m:
+            e = j + 1
+            while e < k and ov[r, e - 1] - ov[r, e] <= eps:
+                e += 1
+            if e <= m and sorted(i_got[r, j:e].tolist()) != sorted(oi[r, j:e].tolist()):
+                raise ParityError(f"row {r}: positions {j}..{e - 1} hold {i_got[r, j:e].tolist()}, "
+                                  f"the oracle {oi[r, j:e].tolist()}")
+            j = e

@@ -16,3 +16,19 @@ for p in (str(REPO), str(PKG)):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD Instinct MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="module")
+def eng():
+    """The gfx950 engine through its C-ABI.  Skips only off an MI355X; on one, a
+    library that fails to load, or was built from other sources than this
+    tree's, fails the test instead of skipping it."""
+    from cuda_vector_search import _ext
+
+    if not _ext.device_supported():
+        pytest.skip("needs an AMD Instinct MI355X (gfx950)")
+    e = _ext.load()
+    maps = Path("/proc/self/maps").read_text()
+    assert str(_ext.LIBRARY) in maps, "libcvs_hip.so from this tree is not mapped"
+    assert _ext.is_current(), "libcvs_hip.so was not built from this tree's sources"
+    return e

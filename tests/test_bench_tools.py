@@ -72,13 +72,9 @@ def test_sweep_summary():
 
 
 @pytest.mark.gpu
-def test_bench_grid_row_schema():
+def test_bench_grid_row_schema(eng):
     import torch
 
-    from cuda_vector_search import _ext
-
-    if not _ext.available():
-        pytest.skip("needs an AMD Instinct MI355X (gfx950)")
     bench = load("bench_gpu")
     rows, gemm = bench.bench_grid([20000], [128], [1, 8], [10], ["fused", "twopass", "torch"],
                                   target_s=0.01, log=lambda s: None)

@@ -3,7 +3,9 @@
 Restates the reference's GPU tests (tests/test_search.py:47-169) against the
 oracle instead of torch, and adds: the committed golden vectors, the batch-1
 GEMV path, the sampling pre-pass on/off, list compaction under adversarial
-ordering, exact ties, and BASELINE-sized shapes checked on a query subset.
+ordering, exact ties, the BASELINE configs at full size (every query at
+C1, C3 and C5, 64 spread queries at C2 and C4, both exact paths), and an
+int8 companion kept current when the corpus changes.
 
 Bars (the north star's): ids identical except inside the 1e-3 near-tie band of
 the k-th score, scores within 1e-3 (oracle.check_exact); score matrices within
@@ -25,17 +27,6 @@ from cuda_vector_search import Index, _ext, synthetic
 pytestmark = pytest.mark.gpu
 
 GOLDEN = sorted((Path(__file__).parent / "golden").glob("*.npz"))
-
-
-@pytest.fixture(scope="module")
-def eng():
-    if not _ext.available():
-        pytest.skip("needs an AMD Instinct MI355X (gfx950)")
-    e = _ext.load()
-    # the in-tree library is what runs
-    maps = Path("/proc/self/maps").read_text()
-    assert str(_ext.LIBRARY) in maps, "libcvs_hip.so from this tree is not mapped"
-    return e
 
 
 def say(*a):
@@ -337,8 +328,10 @@ def test_exact_duplicates_and_near_ties(eng):
         v, i, _ = run_fused(eng, q, x, k)
         oracle.check_exact(q, x, k, v, i)
         ov, oi = oracle.topk(q, x, k)
-        # the engine's scores are fp32 sums in another order; where the oracle's
-        # k-th score is separated from the (k+1)-th, ids must agree exactly
+        # the engine's scores are fp32 sums in another order: above the band of
+        # the k-th score its ids are the oracle's, in the oracle's order except
+        # among rows whose scores agree to 1e-5; exact ties come in id order
+        oracle.check_order(v, i, ov, oi)
         for r in range(q.shape[0]):
             for j in range(k - 1):
                 if v[r, j] == v[r, j + 1]:
@@ -348,8 +341,26 @@ def test_exact_duplicates_and_near_ties(eng):
 # --------------------------------------------------------------------------- full-size shapes
 
 
+def _spread_queries(b: int, want: int = 64) -> np.ndarray:
+    """Query indices for the parity check of a full-size batch: every query when
+    b <= 256 and the oracle is cheap enough (the caller decides), else ``want``
+    spread over every query group and wave of the scan (32 consecutive queries
+    per wave) with a different lane column in each."""
+    if b <= want:
+        return np.arange(b)
+    per = max(1, want // (b // 32))
+    sel = [32 * w + (7 * j + 3 * w) % 32 for w in range(b // 32) for j in range(per)]
+    return np.unique(np.asarray(sel))[:want]
+
+
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
-def test_baseline_configs_on_query_subset(eng, name):
+def test_baseline_configs_full_size(eng, name):
+    """The five BASELINE configs at full size, through Index.search (auto: the
+    int8 pre-filter at C2-C4, the fp16 scan at C1/C5) and method="fused":
+    every query at C1, C3 and C5 (the near-tie config), 64 queries spread over
+    every query group, wave and lane column at C2 and C4; ids and scores at the
+    oracle's bar, ids in the oracle's order above the near-tie band, and the
+    int8 path's ids equal the fp16 path's except between scores within 2e-6."""
     n, d, b, k, ties = synthetic.CONFIGS[name]
     say(f"baseline config {name}: n={n} d={d} b={b} k={k}")
     x = synthetic.unit_corpus(n, d, seed=d, device="cuda")
@@ -358,19 +369,29 @@ def test_baseline_configs_on_query_subset(eng, name):
     q = synthetic.unit_queries(b, d, seed=1, device="cuda")
     index = Index(x, metric="cosine", copy=False)
     qq = index._prep_queries(q)
-    v, i = index.search(q, k)
+    va, ia = index.search(q, k)
+    vf, i_f = index.search(q, k, method="fused")
     torch.cuda.synchronize()
-    # size-independent properties over every query
-    assert bool((v[:, :-1] >= v[:, 1:]).all())
-    ii = i.cpu()
-    assert all(len(set(r)) == k for r in ii.tolist())
-    assert int(ii.min()) >= 0 and int(ii.max()) < n
-    # parity with the oracle on a subset of queries (8, as the reference bench)
-    sel = torch.arange(min(8, b)) * max(1, b // 8)
+    for v, i in ((va, ia), (vf, i_f)):  # size-independent properties over every query
+        assert bool((v[:, :-1] >= v[:, 1:]).all())
+        ii = i.cpu()
+        assert all(len(set(r)) == k for r in ii.tolist())
+        assert int(ii.min()) >= 0 and int(ii.max()) < n
+    # the two exact paths agree (they differ only in the fp32 sum order)
+    va_, ia_, vf_, if_ = (t.cpu().numpy() for t in (va, ia, vf, i_f))
+    np.testing.assert_allclose(va_, vf_, rtol=0, atol=2e-6)
+    same = ia_ == if_
+    assert same.all() or np.abs(va_ - vf_)[~same].max() < 2e-6
+    sel = np.arange(b) if name in ("C1", "C3", "C5") else _spread_queries(b)
+    say(f"  oracle on {len(sel)} of {b} queries")
     xc = index.embeddings.cpu()
-    qc = qq[sel, :index.dim].cpu()
-    oracle.check_exact(qc, xc, k, v[sel].cpu(), ii[sel])
-    del x, index
+    qc = qq[torch.from_numpy(sel).cuda(), :index.dim].cpu()
+    full = oracle.scores(qc, xc)
+    ov, oi = oracle.topk(qc, xc, k)
+    for v, i in ((va_, ia_), (vf_, if_)):
+        oracle.check_exact(qc, xc, k, v[sel], i[sel], full=full)
+        oracle.check_order(v[sel], i[sel], ov, oi)
+    del x, index, full
     torch.cuda.empty_cache()
 
 
@@ -418,9 +439,12 @@ def test_prep_rows_errors(eng):
     x = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
     with pytest.raises(RuntimeError, match="destination width"):
         eng.prep_rows(x, torch.zeros(4, 32, dtype=torch.float16, device="cuda"), True)
-    with pytest.raises(RuntimeError, match="row width"):
-        eng.prep_rows(torch.zeros(4, 2000, dtype=torch.float16, device="cuda"),
-                      torch.zeros(4, 2048, dtype=torch.float16, device="cuda"), True)
+    # any width is accepted now (rows wider than 1536 take the two-pass kernel);
+    # a source stride shorter than the row is still refused, before any launch
+    wide = torch.zeros(4, 2048, dtype=torch.float16, device="cuda")
+    rc = eng.lib.cvs_prep_rows(wide.data_ptr(), wide.data_ptr(), 4, 2048, 1000, 2048, 1,
+                               wide.device.index, None)
+    assert rc != 0 and b"source row stride" in eng.lib.cvs_last_error()
     with pytest.raises(RuntimeError, match="fp16 CUDA"):
         eng.prep_rows(x.float(), x, True)
 
@@ -830,3 +854,53 @@ def test_concurrent_searches_on_threads_and_streams(eng):
     for t, res in enumerate(results):
         for a, b in res:
             assert torch.equal(a, expect[t][0]) and torch.equal(b, expect[t][1])
+
+
+@pytest.mark.gpu
+def test_int8_companion_follows_corpus_changes(eng):
+    """With copy=False the index stores the caller's tensor (as the reference
+    does); rows changed in place afterwards, through that tensor or through
+    Index.embeddings, must not leave the int8 companion stale: "auto" and
+    "int8" rebuild it and stay exact against the current rows, also when
+    several threads search at once after a change."""
+    import threading
+
+    n, d = (1 << 18) + 77, 384
+    say(f"int8 companion after corpus changes n={n}")
+    x = synthetic.unit_corpus(n, d, seed=3, device="cuda")
+    q = synthetic.unit_queries(8, d, seed=4, device="cuda")
+    index = Index(x, metric="ip", copy=False)
+    assert index._x.data_ptr() == x.data_ptr() and index._xq is not None
+    assert index.int8_bytes == eng.q8_corpus_bytes(n, d)
+    index.search(q, 10, method="int8")  # companion of the original rows in use
+    x[123457] = q[0]          # through the caller's tensor
+    index.embeddings[98765] = q[1]  # through the stored rows' view
+    for method in ("auto", "int8"):
+        nq = 1 if method == "auto" else 8  # batch 1: "auto" takes the int8 GEMV here
+        v, i = index.search(q[:nq], 10, method=method)
+        assert int(i[0, 0]) == 123457
+        if nq > 1:
+            assert int(i[1, 0]) == 98765
+        oracle.check_exact(q[:nq].cpu(), x.cpu(), 10, v, i)
+    x[5] = q[2]
+    results, errors = [None] * 4, []
+
+    def work(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                r = index.search(q, 10, method="int8")
+                s.synchronize()
+            results[t] = r
+        except Exception as exc:  # reported below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for v, i in results:
+        assert int(i[2, 0]) == 5
+        oracle.check_exact(q.cpu(), x.cpu(), 10, v, i)

@@ -160,6 +160,33 @@ def test_check_exact_accepts_oracle_and_rejects_planted_mistakes():
         oracle.check_exact(q, x, k - 1, v[:, :k - 1], i[:, 1:])  # best id missing
 
 
+def test_check_order_accepts_oracle_and_rejects_planted_mistakes():
+    """check_order: the oracle's own output and reorderings among near-equal
+    scores pass; two well-separated ids swapped, or a returned set that is right
+    but misordered above the band, fail."""
+    rng = np.random.default_rng(11)
+    x, q = unit(rng, 4000, 96), unit(rng, 5, 96)
+    x[100] = x[200] = x[300] = q[0]  # three exact duplicates: the top three of query 0
+    k = 15
+    v, i = oracle.topk(q, x, k)
+    oracle.check_order(v, i, v, i)
+    assert i[0, :3].tolist() == [100, 200, 300]
+    tie = i.copy()
+    tie[0, :3] = [300, 100, 200]  # any order among the equal scores
+    oracle.check_order(v, tie, v, i)
+    swapped = i.copy()
+    gaps = np.diff(v[1])
+    j = int(np.argmin(gaps))  # the largest gap between neighbours (scores descend)
+    assert v[1, j] - v[1, j + 1] > 1e-5 and v[1, j + 1] > v[1, -1] + 1e-3
+    swapped[1, [j, j + 1]] = swapped[1, [j + 1, j]]
+    with pytest.raises(oracle.ParityError):
+        oracle.check_order(v, swapped, v, i)
+    wrong = i.copy()
+    wrong[2, 0] = i[2, -1]  # a band id in first place instead of the best
+    with pytest.raises(oracle.ParityError):
+        oracle.check_order(v, wrong, v, i)
+
+
 # --------------------------------------------------------------------------- row preparation
 
 
