@@ -515,6 +515,66 @@ int cvs_fused_topk_timed(const void* q, const void* x, int64_t nq, int64_t n, in
   return rc;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Workspace of cvs_fused_topk_noalloc: one array per GPU the library runs on,
+// held until the process ends.  Its name is a host-side stand-in; host code
+// uses only the device address hipGetSymbolAddress returns for the current
+// device (g_scratch_ptr), taken once per device on the entry point's first call.
+constexpr int64_t kScratchBytes = CVS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+void* g_scratch_ptr[kMaxDevices] = {};
+std::once_flag g_scratch_once[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (the caller has made it current).
+int scratch_for(int device, void** out) {
+  std::call_once(g_scratch_once[device], [device] {
+    void* p = nullptr;
+    g_scratch_err[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (g_scratch_err[device] == hipSuccess) g_scratch_ptr[device] = p;
+  });
+  if (g_scratch_err[device] != hipSuccess) return hip_fail(g_scratch_err[device], "hipGetSymbolAddress(scratch)");
+  *out = g_scratch_ptr[device];
+  return CVS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cvs_fused_topk_noalloc(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                           int flags, float* out_v, void* out_i, int64_t* plan_out, int device, void* stream) {
+  DevInfo di;
+  int rc = dev_info(device, &di);
+  if (rc != CVS_OK) return rc;
+  if (!di.gfx950) return fail(CVS_ERR_INVALID, "libcvs_hip targets gfx950 (MI355X); device %d is %s", device, di.arch);
+  rc = check_inputs(q, x, nq, n, d);
+  if (rc != CVS_OK) return rc;
+  Plan P;
+  rc = make_plan(nq, n, d, k, 0, 0, flags, di.cus, &P);
+  if (rc != CVS_OK) return rc;
+  if (P.ws_bytes > kScratchBytes)
+    return fail(CVS_ERR_INVALID,
+                "the allocation-free search needs %lld bytes of workspace for these sizes, more than its "
+                "%lld-byte scratch: use cvs_fused_topk with a workspace",
+                (long long)P.ws_bytes, (long long)kScratchBytes);
+  void* ws = nullptr;
+  {
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+    rc = scratch_for(device, &ws);
+    if (rc != CVS_OK) return rc;
+  }
+  // The fused path needs no zeroed workspace (every list count and threshold is
+  // written before it is read), so nothing is cleared here.
+  return run_fused(q, x, nq, n, d, k, 0, 0, flags, ws, kScratchBytes, out_v, out_i, plan_out, device, stream,
+                   nullptr);
+}
+
 int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
                           int64_t bq, int64_t chunks, int flags, void* workspace,
                           int64_t workspace_bytes, float* out_v, void* out_i, int64_t* plan_out,

@@ -44,6 +44,7 @@ FLAG_NO_PREPASS = 1
 FLAG_FORCE_PREPASS = 2
 FLAG_NO_GEMV = 4
 FLAG_IDS_INT64 = 8  # ids as int64 (Index.search's dtype) instead of the reference's int32
+NOALLOC_SCRATCH_BYTES = 96 << 20  # CVS_NOALLOC_SCRATCH_BYTES: scratch of cvs_fused_topk_noalloc per GPU
 
 
 def device_supported() -> bool:
@@ -130,6 +131,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.cvs_fused_topk_timed.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp, i64,
                                          vp, vp, ctypes.POINTER(i64), i32, vp,
                                          ctypes.POINTER(ctypes.c_float)]
+    lib.cvs_fused_topk_noalloc.restype = i32
+    lib.cvs_fused_topk_noalloc.argtypes = [vp, vp, i64, i64, i64, i64, i32, vp, vp, ctypes.POINTER(i64), i32, vp]
     lib.cvs_topk_rows.restype = i32
     lib.cvs_topk_rows.argtypes = [vp, i64, i64, i64, i32, vp, i64, vp, vp, i32, vp]
     lib.cvs_topk_rows_plan.restype = i32

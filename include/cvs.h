@@ -125,6 +125,23 @@ int cvs_fused_topk_marked(const void* q, const void* x, int64_t nq, int64_t n, i
                           int device, void* stream, void* const* marks);
 
 /*
+ * Allocation-free cvs_fused_topk (no counterpart in the reference).  For
+ * callers that cannot allocate device memory at search time: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments, results and errors as cvs_fused_topk with bq = chunks = 0 (the
+ * auto plan), but the workspace is a library-owned device array of
+ * CVS_NOALLOC_SCRATCH_BYTES per GPU (set up on the first call on a device,
+ * held until the process ends); calls whose plan needs more (cvs_fused_plan's
+ * workspace_bytes) fail with CVS_ERR_INVALID.  It calls no hipMalloc/hipFree.
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must be serialised by the caller.
+ * Covers the headline shapes (1M x 384, batch 256, k 10: 67.1 MB).
+ */
+#define CVS_NOALLOC_SCRATCH_BYTES (96ll << 20)
+int cvs_fused_topk_noalloc(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, int64_t k,
+                           int flags, float* out_v, void* out_i, int64_t* plan_out, int device, void* stream);
+
+/*
  * Exact top-k of each row of an fp32 matrix scores[nq, n] (row-major): the k
  * largest values of each row with their column indices, sorted by value
  * descending then index ascending (the fused path's order).  1 <= k <= 1024,
