@@ -22,10 +22,23 @@ config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
   measured HBM bytes per launch: two child runs of this script under
   ``rocprofv3 --pmc`` (FETCH_SIZE, then WRITE_SIZE), each scaled by what the
   same counter reads for a plain 1 GiB device copy in the same child;
+* configs_detail: one row per config with the same W warm-up and K timed calls:
+  ms per batch, queries/s, per-stage device times, the dominant kernel's
+  fraction of its roofline on its own bytes, and the end-to-end roofline of
+  BASELINE.md section 2 (achieved = max(F/P_fp16, B/BW) / t with F = 2 b n d,
+  B = 2 n d + 2 b d + 12 b k, both component fractions), plus that config's
+  CPU baseline;
 * cpu_baseline: the reference's CPU search path (fp32 torch matmul + topk,
   reference.py:8-15) and the numpy baseline (bench/bench_baselines.py:45-50),
-  both as restated in oracle/, timed on this host on a bounded sample of the
-  same workload; their results double as the recall check of the GPU output.
+  both as restated in oracle/, timed on this host on a bounded sample of each
+  config's batch (time_call semantics of bench/timing.py:9-34 with the CPU
+  settings of bench/bench_baselines.py:125-127); their results double as the
+  recall check of the GPU output.
+
+Warm-up: after the GPU has idled (data generation) or run other work, the
+first ~25-50 searches of the C2 int8 path run 7-10% slower whatever this
+library does (measured per call: the same after 2 s idle and after a matmul
+burn, nothing at the cache-resident C1); W defaults to 20.
 """
 
 from __future__ import annotations
@@ -63,6 +76,24 @@ def kernel_bytes(n, d, b):
 def kernel_bytes_q8(n, dq, b):
     """Algorithmic HBM bytes of one int8 scan/GEMV launch: int8 corpus once + int8 queries."""
     return n * dq + b * dq
+
+
+def end_to_end(n, d, b, k, ms, int8, dq):
+    """the whole search against max(F/P, B/BW) with
+    F = 2 b n d (fp16 MFMA peak) and B = 2 n d + 2 b d + 12 b k (the fp16
+    corpus read once), whatever path ran; both component fractions."""
+    f = 2.0 * b * n * d
+    nbytes = 2.0 * n * d + 2.0 * b * d + 12.0 * b * k
+    t_mfma = f / MFMA_FP16_PEAK
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    t = ms * 1e-3
+    out = {"flops": f, "bytes": nbytes, "t_mfma_us": round(t_mfma * 1e6, 2), "t_hbm_us": round(t_hbm * 1e6, 2),
+           "achieved": round(max(t_mfma, t_hbm) / t, 4), "mfma_frac": round(t_mfma / t, 4),
+           "hbm_frac": round(t_hbm / t, 4)}
+    if int8:
+        out["note"] = (f"the int8 path streams n*{dq} bytes of int8 companion instead of the 2*n*d fp16 bytes "
+                       "counted in B, plus the fp16 rows of the candidates it rescores")
+    return out
 
 
 def run_config(name, steps, warmup, eng, torch, synthetic, Index):
@@ -151,6 +182,7 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
         "kernel_hbm_gbs": round(gbs, 1), "kernel_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "kernel_mfma_frac": round(flops / (kern_ms * 1e-3) / mfma_peak, 4),
         "roofline_floor_us": round(max(flops / mfma_peak, nbytes / (HBM_PEAK_GBS * 1e9)) * 1e6, 2),
+        "end_to_end": end_to_end(n, d, b, k, wall_ms, int8, dq),
         "other_path": {"path": "fused" if int8 else "int8",
                        "ms_per_batch": round(alt_ms, 4) if alt_ms is not None else None},
     }
@@ -254,32 +286,7 @@ def measure_traffic(name):
     return int(round(traffic)), res
 
 
-def cpu_baseline(index, q, k, gpu_ids, torch, sample_q=32, target_s=10.0):
-    """The reference's CPU paths on a bounded sample: all corpus rows, the first
-    `sample_q` queries.  Restated in oracle/ (kind "port")."""
-    import numpy as np
-
-    import oracle
-
-    threads = torch.get_num_threads()
-    xf = index.embeddings.float().cpu().contiguous()          # CPU Index stores fp32 (index.py:69)
-    qf = q[:sample_q].float().cpu().contiguous()
-    xn, qn = xf.numpy(), qf.numpy()
-
-    def timed(fn):
-        fn()  # warm-up
-        times = []
-        t_end = time.perf_counter() + target_s
-        while (time.perf_counter() < t_end and len(times) < 20) or len(times) < 3:
-            t0 = time.perf_counter()
-            res = fn()
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times), len(times), res
-
-    t_torch, reps_t, (tv, ti) = timed(lambda: oracle.torch_topk_cpu(qf, xf, k))
-    t_np, reps_n, (nv, ni) = timed(lambda: oracle.numpy_search(qn, xn, k))
-    gi = gpu_ids[:sample_q].cpu().numpy()
-    recall = float(np.mean([len(set(a) & set(b)) / k for a, b in zip(gi.tolist(), ti.numpy().tolist())]))
+def _host_facts(torch):
     cpu_model = ""
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -288,13 +295,78 @@ def cpu_baseline(index, q, k, gpu_ids, torch, sample_q=32, target_s=10.0):
                 break
     except OSError:
         pass
+    blas = ""
+    try:
+        import numpy as np
+
+        cfg = np.show_config(mode="dicts")
+        blas = cfg.get("Build Dependencies", {}).get("blas", {}).get("name", "")
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return {"host_cpu": cpu_model, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "numpy_blas": blas}
+
+
+def _mem_available_bytes():
+    try:
+        for line in Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return None
+
+
+def time_cpu(fn, target_s=1.0, max_reps=20):
+    """Median seconds per call with bench/timing.py:9-34's semantics at the CPU
+    settings of bench/bench_baselines.py:125-127: 2 warm-up calls (1 if a call
+    takes more than a second), then calls until target_s or max_reps, at least 3."""
+    t0 = time.perf_counter()
+    res = fn()
+    if time.perf_counter() - t0 <= 1.0:
+        res = fn()
+    times = []
+    t_end = time.perf_counter() + target_s
+    while (time.perf_counter() < t_end and len(times) < max_reps) or len(times) < 3:
+        t1 = time.perf_counter()
+        res = fn()
+        times.append(time.perf_counter() - t1)
+    return statistics.median(times), len(times), res
+
+
+def cpu_baseline(index, q, k, gpu_ids, torch, sample_q=64):
+    """The reference's CPU paths for one config on a bounded sample: every
+    corpus row, the first `sample_q` queries of the batch.  Restated in oracle/
+    (kind "port"): the CPU Index's fp32 torch matmul + topk (reference.py:8-15,
+    index.py:69) and numpy matmul + argpartition (bench_baselines.py:45-50)."""
+    import numpy as np
+
+    import oracle
+
+    n, dim = index.embeddings.shape
+    need = n * dim * 4 * 2  # the fp32 corpus, and headroom for its score rows and copies
+    avail = _mem_available_bytes()
+    if avail is not None and need > 0.5 * avail:
+        return {"value": None, "unit": "queries/s", "kind": "port",
+                "skipped": f"fp32 corpus {n}x{dim} needs ~{need / 1e9:.1f} GB; host has {avail / 1e9:.1f} GB "
+                           "available"}
+    threads = torch.get_num_threads()
+    sq = min(sample_q, q.shape[0])
+    xf = index.embeddings.float().cpu().contiguous()
+    qf = q[:sq, :dim].float().cpu().contiguous()
+    xn, qn = xf.numpy(), qf.numpy()
+    t_torch, reps_t, (tv, ti) = time_cpu(lambda: oracle.torch_topk_cpu(qf, xf, k))
+    t_np, reps_n, _ = time_cpu(lambda: oracle.numpy_search(qn, xn, k))
+    gi = gpu_ids[:sq].cpu().numpy()
+    recall = float(np.mean([len(set(a) & set(b)) / k for a, b in zip(gi.tolist(), ti.numpy().tolist())]))
+    del xf, xn
     return {
-        "value": round(sample_q / t_torch, 2), "unit": "queries/s", "cores": threads, "kind": "port",
-        "sample": f"{sample_q} of the batch's queries against the full corpus ({xf.shape[0]}x{xf.shape[1]} fp32); "
+        "value": round(sq / t_torch, 2), "unit": "queries/s", "cores": threads, "kind": "port",
+        "sample": f"{sq} of the batch's {q.shape[0]} queries against the full corpus ({n}x{dim} fp32); "
                   f"torch matmul+topk (reference.py:8-15), median of {reps_t}",
-        "numpy_argpartition_qps": round(sample_q / t_np, 2),
+        "ms_per_query": round(t_torch / sq * 1e3, 4),
+        "numpy_argpartition_qps": round(sq / t_np, 2),
         "numpy_sample": f"same sample, numpy matmul+argpartition (bench_baselines.py:45-50), median of {reps_n}",
-        "host_cpu": cpu_model, "os_cpu_count": os.cpu_count(),
         "gpu_recall_vs_cpu_torch": round(recall, 5),
     }
 
@@ -303,12 +375,13 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=200,
-                    help="untimed steps first (the first ~100 calls after start-up run ~15%% slower)")
+    ap.add_argument("--warmup", type=int, default=20,
+                    help="untimed steps before each config's timed ones")
     ap.add_argument("--configs", default="C2,C1,C3,C4,C5",
                     help="first entry is the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-queries", type=int, default=64,
+                    help="queries of each batch in the CPU baseline's sample (all of a smaller batch)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     ap.add_argument("--pmc-child", metavar="CONFIG", help=argparse.SUPPRESS)
@@ -342,25 +415,22 @@ def main():
     eng = _ext.load()
 
     rows = []
-    head = None
+    cpu = None
     for i, name in enumerate(names):
-        row, state = run_config(name, args.steps if i == 0 else max(5, args.steps // 5),
-                                args.warmup if i == 0 else max(2, args.warmup // 4),
-                                eng, torch, synthetic, Index)
+        # every config gets the same warm-up and timed steps
+        row, state = run_config(name, args.steps, args.warmup, eng, torch, synthetic, Index)
+        if not args.no_cpu_baseline:
+            index, q, k, out = state
+            log(f"[{name}] cpu baseline ...")
+            row["cpu_baseline"] = cpu_baseline(index, q, k, out[1], torch, sample_q=args.cpu_queries)
+            log(f"[{name}] cpu baseline {json.dumps(row['cpu_baseline'])}")
+            if i == 0:
+                cpu = dict(row["cpu_baseline"], **_host_facts(torch))
         rows.append(row)
-        if i == 0:
-            head = (row, state)
-            if not args.no_cpu_baseline:
-                index, q, k, out = state
-                log(f"[{name}] cpu baseline ...")
-                cpu = cpu_baseline(index, q, k, out[1], torch, target_s=args.cpu_seconds)
-                log(f"[{name}] cpu baseline {json.dumps(cpu)}")
-            else:
-                cpu = None
-            del state
+        del state
         torch.cuda.empty_cache()
 
-    row = head[0]
+    row = rows[0]
     n, d, b, k = row["n"], row["d"], row["batch"], row["k"]
     kern_ms = row["stage_ms"]["scan" if b > 1 else "gemv"]
     out = {
@@ -393,6 +463,7 @@ def main():
             "kernel_ms": kern_ms,
             "algorithmic_bytes": row["kernel_bytes"],
             "mfma_frac": row["kernel_mfma_frac"],
+            "end_to_end": row["end_to_end"],
         },
         "cpu_baseline": cpu,
         "configs_detail": rows,

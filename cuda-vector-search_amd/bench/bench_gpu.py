@@ -17,6 +17,8 @@ from __future__ import annotations
 
 import argparse
 import datetime as dt
+import functools
+import itertools
 import json
 import os
 import platform
@@ -55,56 +57,71 @@ def env_info() -> dict:
     }
 
 
-def bench_grid(sizes, dims, batches, ks, methods, seed=0, target_s=0.3, log=print):
+def _mb(nbytes: int) -> float:
+    return round(nbytes / 2**20, 1)
+
+
+def measure_cell(index, q, k, method, ref_ids, target_s):
+    """One grid cell: peak extra device memory of a first call, recall of its ids
+    on the reference's queries, then the median synced wall time.  Returns the
+    row fields (or {"error": "OOM"})."""
     sync = torch.cuda.synchronize
+    run = functools.partial(index.search, q, k, method=method)
+    sync()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    try:
+        ids = run()[1]
+        sync()
+        extra = torch.cuda.max_memory_allocated() - before
+        checked = min(len(ref_ids), q.shape[0])
+        found = recall(ids[:checked].cpu().tolist(), [r[:k] for r in ref_ids[:checked]])
+        ms, reps = time_call(run, sync, target_s=target_s)
+    except torch.cuda.OutOfMemoryError:
+        torch.cuda.empty_cache()
+        return {"error": "OOM"}
+    return {"extra_mem_mb": _mb(extra), "recall_vs_fp32": found, "ms": round(ms, 4),
+            "qps": round(q.shape[0] * 1000.0 / ms, 1), "reps": reps}
+
+
+def score_kernel_vs_blas(index, q, target_s):
+    """The gfx950 score kernel (fp16 score matrix) against the vendor BLAS behind
+    torch.matmul on the same prepared operands."""
+    eng = _ext.load()
+    qp = index._prep_queries(q)
+    sync = torch.cuda.synchronize
+    ours, _ = time_call(lambda: eng.scores(qp, index._x, False), sync, target_s=target_s)
+    blas, _ = time_call(lambda: torch.matmul(qp, index._x.T), sync, target_s=target_s)
+    n, d, b = len(index), index.dim, q.shape[0]
+    tera = 2.0 * b * n * d / 1e12
+    return {"n": n, "d": d, "batch": b, "custom_ms": round(ours, 3), "cublas_ms": round(blas, 3),
+            "custom_tflops": round(tera / (ours / 1e3), 2), "cublas_tflops": round(tera / (blas / 1e3), 2),
+            "blas": "hipBLASLt (torch.matmul)"}
+
+
+def bench_grid(sizes, dims, batches, ks, methods, seed=0, target_s=0.3, log=print):
+    """Every (n, d) corpus that fits, then every (batch, k, method) cell on it;
+    one score-kernel comparison per corpus at the largest batch."""
     rows, gemm = [], []
-    total_mem = torch.cuda.get_device_properties(0).total_memory
-    for d in dims:
-        for n in sizes:
-            need = 3 * n * d + 4 * max(batches) * n + (1 << 30)  # fp16 corpus + int8 companion + scores
-            if need > total_mem:
-                rows.append({"n": n, "d": d, "skipped": "memory"})
-                continue
-            torch.cuda.empty_cache()
-            x = synthetic.unit_corpus(n, d, seed=seed + d, device="cuda")
-            index = Index(x, metric="ip", copy=False)
-            qall = synthetic.unit_queries(max(batches), d, seed=seed + 1, device="cuda")
-            _, ref_i = exact_topk_fp32(qall[:N_REF], x, max(ks))
-            ref_i = ref_i.cpu()
-            for b in batches:
-                q = qall[:b].contiguous()
-                for k in ks:
-                    for m in methods:
-                        row = {"n": n, "d": d, "batch": b, "k": k, "method": m}
-                        try:
-                            sync()
-                            torch.cuda.reset_peak_memory_stats()
-                            base = torch.cuda.memory_allocated()
-                            _, ids = index.search(q, k, method=m)
-                            sync()
-                            row["extra_mem_mb"] = round((torch.cuda.max_memory_allocated() - base) / 2**20, 1)
-                            nr = min(N_REF, b)
-                            row["recall_vs_fp32"] = recall(ids[:nr].cpu().tolist(), ref_i[:nr, :k].tolist())
-                            ms, reps = time_call(lambda: index.search(q, k, method=m), sync, target_s=target_s)
-                            row.update(ms=round(ms, 4), qps=round(b / (ms / 1000), 1), reps=reps)
-                        except torch.cuda.OutOfMemoryError:
-                            row["error"] = "OOM"
-                            torch.cuda.empty_cache()
-                        log(json.dumps(row))
-                        rows.append(row)
-            b = max(batches)
-            qp = index._prep_queries(qall[:b].contiguous())
-            eng = _ext.load()
-            ms_c, _ = time_call(lambda: eng.scores(qp, index._x, False), sync, target_s=target_s)
-            ms_b, _ = time_call(lambda: qp @ index._x.T, sync, target_s=target_s)
-            flops = 2.0 * b * n * d
-            g = {"n": n, "d": d, "batch": b, "custom_ms": round(ms_c, 3), "cublas_ms": round(ms_b, 3),
-                 "custom_tflops": round(flops / ms_c / 1e9, 2), "cublas_tflops": round(flops / ms_b / 1e9, 2),
-                 "blas": "hipBLASLt (torch.matmul)"}
-            log(json.dumps(g))
-            gemm.append(g)
-            del x, index, qall, qp
-            torch.cuda.empty_cache()
+    dev_bytes = torch.cuda.get_device_properties(0).total_memory
+    for d, n in itertools.product(dims, sizes):
+        # fp16 corpus + int8 companion + the largest score matrix + slack
+        if 3 * n * d + 4 * max(batches) * n + (1 << 30) > dev_bytes:
+            rows.append({"n": n, "d": d, "skipped": "memory"})
+            continue
+        torch.cuda.empty_cache()
+        index = Index(synthetic.unit_corpus(n, d, seed=seed + d, device="cuda"), metric="ip", copy=False)
+        queries = synthetic.unit_queries(max(batches), d, seed=seed + 1, device="cuda")
+        ref_ids = exact_topk_fp32(queries[:N_REF], index.embeddings, max(ks))[1].cpu().tolist()
+        for b, k, method in itertools.product(batches, ks, methods):
+            row = {"n": n, "d": d, "batch": b, "k": k, "method": method}
+            row.update(measure_cell(index, queries[:b].contiguous(), k, method, ref_ids, target_s))
+            log(json.dumps(row))
+            rows.append(row)
+        gemm.append(score_kernel_vs_blas(index, queries, target_s))
+        log(json.dumps(gemm[-1]))
+        del index, queries
+        torch.cuda.empty_cache()
     return rows, gemm
 
 

@@ -23,13 +23,15 @@ def short_n(n: int) -> str:
 
 
 def merge(paths):
-    env, rows, gemm = {}, [], []
-    for p in paths:
-        data = json.loads(Path(p).read_text())
-        for key, val in data.get("env", {}).items():
-            env.setdefault(key, val)
-        rows.extend(r for r in data.get("rows", []) if "method" in r)
-        gemm.extend(data.get("gemm", []))
+    """(env, rows, gemm) of several result files: rows and score-kernel rows of
+    all of them (grid rows only: skipped corpora carry no method), and the
+    environment with the first file's value wherever two files disagree."""
+    docs = [json.loads(Path(p).read_text()) for p in paths]
+    env = {}
+    for doc in reversed(docs):
+        env.update(doc.get("env", {}))
+    rows = [r for doc in docs for r in doc.get("rows", []) if "method" in r]
+    gemm = [g for doc in docs for g in doc.get("gemm", [])]
     return env, rows, gemm
 
 

@@ -11,6 +11,7 @@ the chunk count at 1/4 .. 4x of the automatic plan.  Prints the best plan per
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import sys
 from pathlib import Path
@@ -24,36 +25,40 @@ from cuda_vector_search import _ext, synthetic  # noqa: E402
 from timing import time_call  # noqa: E402
 
 
+def candidate_plans(auto_chunks: int, batch: int):
+    """Forced (bq, chunks) plans around the automatic one: every query block the
+    batch can fill at least half of (16 always), chunk counts from a quarter to
+    four times the automatic count in powers of two."""
+    blocks = [bq for bq in (16, 32, 64, 128, 256) if bq == 16 or 2 * batch >= bq]
+    scales = [2.0 ** e for e in range(-2, 3)]
+    return [(bq, max(1, int(auto_chunks * f))) for bq in blocks for f in scales]
+
+
 def sweep(n, d, batches=(1, 32, 256), ks=(10, 100, 256), target_s=0.15, log=print):
     eng = _ext.load()
     x = synthetic.unit_corpus(n, d, seed=d, device="cuda")
     qall = synthetic.unit_queries(max(batches), d, seed=1, device="cuda")
+    sync = torch.cuda.synchronize
     rows = []
-    for b in batches:
+
+    def timed(q, k, bq, chunks):
+        plan = [int(v) for v in eng.fused_topk(q, x, k, bq, chunks)[2].tolist()]
+        ms, _ = time_call(lambda: eng.fused_topk(q, x, k, bq, chunks), sync, target_s=target_s)
+        return plan, round(ms, 4)
+
+    for b, k in itertools.product(batches, ks):
         q = qall[:b].contiguous()
-        for k in ks:
-            auto = [int(v) for v in eng.fused_topk(q, x, k)[2].tolist()]
-            ms, _ = time_call(lambda: eng.fused_topk(q, x, k), torch.cuda.synchronize, target_s=target_s)
-            r = {"n": n, "d": d, "batch": b, "k": k, "bq": 0, "chunks": 0, "plan": auto, "auto": auto,
-                 "ms": round(ms, 4)}
-            log(json.dumps(r))
-            rows.append(r)
-            for bq in (16, 32, 64, 128, 256):
-                if bq > 16 and b < bq // 2:
-                    continue
-                for f in (0.25, 0.5, 1, 2, 4):
-                    chunks = max(1, int(auto[1] * f))
-                    try:
-                        plan = [int(v) for v in eng.fused_topk(q, x, k, bq, chunks)[2].tolist()]
-                        ms, _ = time_call(lambda: eng.fused_topk(q, x, k, bq, chunks), torch.cuda.synchronize,
-                                          target_s=target_s)
-                    except RuntimeError as e:  # plan not available at this width / k
-                        log(f"skip b={b} k={k} bq={bq} chunks={chunks}: {e}")
-                        continue
-                    r = {"n": n, "d": d, "batch": b, "k": k, "bq": bq, "chunks": chunks, "plan": plan,
-                         "auto": auto, "ms": round(ms, 4)}
-                    log(json.dumps(r))
-                    rows.append(r)
+        auto, auto_ms = timed(q, k, 0, 0)
+        cells = [(0, 0, auto, auto_ms)]
+        for bq, chunks in candidate_plans(auto[1], b):
+            try:
+                cells.append((bq, chunks, *timed(q, k, bq, chunks)))
+            except RuntimeError as e:  # no kernel for this block at this width / k
+                log(f"skip b={b} k={k} bq={bq} chunks={chunks}: {e}")
+        for bq, chunks, plan, ms in cells:
+            rows.append({"n": n, "d": d, "batch": b, "k": k, "bq": bq, "chunks": chunks, "plan": plan,
+                         "auto": auto, "ms": ms})
+            log(json.dumps(rows[-1]))
     return rows
 
 
