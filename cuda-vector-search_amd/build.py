@@ -20,6 +20,9 @@ import sys
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+import hazard_check  # noqa: E402
+
 PKG_ROOT = Path(__file__).resolve().parent
 REPO = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
@@ -76,8 +79,15 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         obj = BUILD / (Path(src).stem + ".o")
         objs.append(obj)
         cmds.append([HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", CSRC / src, "-o", obj])
+    # device assembly of the MFMA kernels, for the result-hazard check below
+    asm = BUILD / "cvs_scan.s"
+    cmds.append([HIPCC, *FLAGS, *EXTRA["cvs_scan.hip"], "--cuda-device-only", "-S", "-c", CSRC / "cvs_scan.hip",
+                 "-o", asm])
     with ThreadPoolExecutor(max_workers=jobs or min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
+    early = hazard_check.check(asm)
+    if early:
+        raise RuntimeError(f"{len(early)} MFMA results read too early in the scan kernels, e.g. " + early[0])
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB)

@@ -51,6 +51,7 @@ struct Mfma<16> {
   typedef f32x4 acc_t;
   static constexpr int KSZ = 32;  // k per instruction
   static constexpr int NE = 4;    // accumulator elements per lane
+  static constexpr int PASSES = 4;  // 16 cycles on gfx950
   __device__ static acc_t run(half8 a, half8 b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
@@ -63,6 +64,7 @@ struct Mfma<32> {
   typedef float acc_t __attribute__((ext_vector_type(16)));
   static constexpr int KSZ = 16;
   static constexpr int NE = 16;
+  static constexpr int PASSES = 8;  // 32 cycles on gfx950
   __device__ static acc_t run(half8 a, half8 b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -79,6 +81,7 @@ struct MfmaI8 {
   typedef int acc_t __attribute__((ext_vector_type(16)));
   static constexpr int KSZ = 16;  // 2-byte units per k-step (32 int8)
   static constexpr int NE = 16;
+  static constexpr int PASSES = 8;
   __device__ static acc_t run(half8 a, half8 b, acc_t c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b),
                                                   c, 0, 0, 0);
@@ -94,6 +97,24 @@ template <>
 struct MfmaFor<32, kAppendQ8> {
   typedef MfmaI8 type;
 };
+
+// Wait states between a tile's last MFMA and the epilogue's first VALU read of
+// its accumulators.  gfx950 needs passes + 4 for a VALU read of an MFMA's VGPR
+// result; with the accumulators in VGPRs (-amdgpu-mfma-vgpr-form) this
+// compiler leaves only passes + 3 between them, and the epilogue then reads a
+// partial sum (the score matrix intermittently lacked the last k-step).  The
+// pad is 2 * passes + 3, tied to the accumulator so that it follows the last
+// MFMA; the build checks every MFMA result read of the scan kernels against
+// passes + 4 (hazard_check.py).
+template <int PASSES, class T>
+__device__ __forceinline__ void pad_mfma_result(T& acc) {
+  constexpr int WS = 2 * PASSES + 3;
+  static_assert(WS > 8 && WS <= 24, "pad of 9..24 wait states");
+  if constexpr (WS > 16)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 17));
+  else
+    asm volatile("s_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 9));
+}
 
 // FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
 // compile-time constant (per-stage guards on a runtime count split the
@@ -554,10 +575,9 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
     // The epilogue's first VALU reads of the accumulators can follow the
     // tile's last MFMA within a few instructions (across the partial-tile
-    // branch).  Pad with 19 wait states (a 16-pass MFMA's result latency)
-    // after the last MFMA; the empty asm statements order every accumulator
-    // read after the padding.
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2" : "+v"(acc[QB - 1][RB - 1]));
+    // branch): pad its result latency (pad_mfma_result); the empty asm
+    // statements order every accumulator read after the padding.
+    pad_mfma_result<M::PASSES>(acc[QB - 1][RB - 1]);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
