@@ -140,10 +140,19 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int BQ = QS * QW;        // queries per workgroup
   constexpr int RW = MS * RB;        // rows per wave per tile
   constexpr int TR = RS * RW;        // tile rows
-  constexpr int KPS = 64 / M::KSZ;   // MFMA k-steps per 64-column stage
+  constexpr int KSL = 64 / M::KSZ;   // MFMA k-steps per 128-byte line of a row
+  // TS (whole-tile stages): when a full-width tile is 24 KB (the int8 scan of
+  // 384-byte rows, 64 rows, 8 waves), a stage is the whole tile, LPR 128-byte
+  // lines per row, and every 1 KB DMA load reads 8 consecutive lines of global
+  // memory (measured: HBM -> LDS at 6.5 TB/s against 5.4 TB/s for stages of one
+  // 128-byte line per row, whose loads read 8 lines a row apart).  Otherwise a
+  // stage is one line (64 columns) of every row of the tile.
+  constexpr bool TS = FULLW && MODE == kAppendQ8 && NW == 8 && TR * KSMAX * M::KSZ * 2 == 24 * 1024;
+  constexpr int LPR = TS ? KSMAX / KSL : 1;  // lines per row in a stage
+  constexpr int KPS = LPR * KSL;     // MFMA k-steps per stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
-  constexpr int FC = TRB * KPS;      // 1 KB DMA loads (8 rows x 128 bytes) of corpus rows per stage
-  static_assert(FC * 8 == TR, "a stage load covers 8 rows of 128 bytes");
+  constexpr int FC = TR * LPR / 8;   // 1 KB DMA loads (8 lines of 128 bytes) of corpus rows per stage
+  static_assert(TRB * KSL * 8 == TR, "an MS-row block is MS lines of 128 bytes");
   // QL (KSMAX == 0, rows of any width): the queries are not held in registers
   // but ride in every stage beside the corpus rows, QA rows of 128 bytes (the
   // query block padded so every wave issues the same number of loads), and the
@@ -177,7 +186,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
   __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
   __shared__ int st_meta[APP ? NW : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
-  __shared__ uint64_t sortbuf[APP ? NW * kMaxCap : 1];  // compaction scratch
+  __shared__ uint64_t sortbuf[MODE == kAppend ? NW * kMaxCap : 1];  // compaction scratch (int8 lists never compact)
   // kStore*: each wave's [QW queries][RW rows] score tile, written out one query
   // row at a time by consecutive lanes (coalesced); rows padded by 4 elements.
   constexpr bool STORE = (MODE == kStoreF32 || MODE == kStoreF16);
@@ -246,8 +255,10 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       src_row[j] = -1;  // never clamped
       src[j] = a.q + (int64_t)min(grp * BQ + ql, a.nq - 1) * d + poff[j];
     } else {
-      const int rl = f * 8 + (lane >> 3);  // tile row of this lane's load
-      poff[j] = ((lane & 7) ^ piece_swz(rl)) * 8;
+      // line L of the stage: row L / LPR of the tile, its line L % LPR
+      const int L = f * 8 + (lane >> 3);
+      const int rl = L / LPR;
+      poff[j] = (L % LPR) * 64 + ((lane & 7) ^ piece_swz(rl)) * 8;
       src_row[j] = t_begin * TR + rl;
       src[j] = a.x + src_row[j] * d + poff[j];
     }
@@ -373,7 +384,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
         // int8 pre-filter: a full list is not compacted (its entries are only
         // bounds); the surplus is dropped and the count, now above cap, marks
         // the list as overflowed so that the select rescans its whole range.
-        if (Q8) todo = 0;
+        if constexpr (Q8) break;
         uint64_t om = __ballot(todo != 0);
         if (!om) break;
 #pragma unroll 1
@@ -411,20 +422,22 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 
   // A fragments of one stage (KPS k-steps x RB row blocks), read from LDS one
   // stage ahead of the MFMAs that consume them.
-  // A fragment of k-step kk, row block rb: row R = (rs*RB + rb)*MS + col, piece
-  // kk*G + kg, at R*128 + ((piece ^ piece_swz(R)) << 4); piece_swz(R) depends on
-  // R mod 16 = col mod 16 only, so one lane offset per k-step serves every rb.
+  // A fragment of k-step kk, row block rb: row R = (rs*RB + rb)*MS + col, its
+  // line kk / KSL, piece (kk % KSL)*G + kg, at (R*LPR + line)*128 +
+  // ((piece ^ piece_swz(R)) << 4); piece_swz(R) depends on R mod 16 = col mod
+  // 16 only, so one lane offset per k-step serves every rb.
   int aoff[KPS];
 #pragma unroll
   for (int kk = 0; kk < KPS; ++kk)
-    aoff[kk] = (rs * RB * MS + col) * 128 + (((kk * G + kg) ^ piece_swz(col)) << 4);
+    aoff[kk] = ((rs * RB * MS + col) * LPR + kk / KSL) * 128 + ((((kk % KSL) * G + kg) ^ piece_swz(col)) << 4);
+  constexpr int RBOFF = MS * LPR * 128;  // LDS bytes between row blocks
   auto read_stage = [&](int buf_idx, half8 (&f)[KPS][RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
     for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
-        f[kk][rb] = *(const half8*)(buf + aoff[kk] + rb * MS * 128);
+        f[kk][rb] = *(const half8*)(buf + aoff[kk] + rb * RBOFF);
   };
   // QL: B fragment of k-step kk, query block qb: query-area row
   // Rq = qs*QW + qb*MS + col (after the TR corpus rows), same piece rule.
@@ -456,7 +469,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   auto read_ks = [&](int buf_idx, int kk, half8 (&f)[RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + aoff[kk] + rb * MS * 128);
+    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + aoff[kk] + rb * RBOFF);
   };
   wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
   __builtin_amdgcn_s_barrier();           // ... and for every wave

@@ -904,3 +904,30 @@ def test_int8_companion_follows_corpus_changes(eng):
     for v, i in results:
         assert int(i[2, 0]) == 5
         oracle.check_exact(q.cpu(), x.cpu(), 10, v, i)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,d,b,k", [(100_000, 384, 32, 10), (200_000, 384, 256, 10), (100_000, 384, 256, 100)])
+def test_searches_on_a_garbage_workspace(eng, n, d, b, k):
+    """The workspace needs no initialisation: searches right after its memory
+    held random bits (the caching allocator hands the same block back) are
+    exact and repeat bit for bit, on the fp16 and int8 paths."""
+    say(f"garbage workspace n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=b + k)
+    qd, xd = q.cuda(), x.cuda()
+    xq = eng.q8_build(xd)
+    _, ws16 = eng.plan(b, n, d, k, device=qd.device.index)
+    _, ws8 = eng.q8_plan(b, n, d, k, device=qd.device.index)
+    outs = []
+    for _ in range(3):
+        for nbytes in (ws16, ws8):
+            junk = torch.randint(-2**62, 2**62, (max(nbytes, 256) // 8 + 1,), dtype=torch.int64, device="cuda")
+            del junk
+            outs.append(eng.fused_topk(qd, xd, k) if nbytes == ws16 else eng.q8_topk(qd, xd, xq, k))
+    torch.cuda.synchronize()
+    v0, i0, _ = outs[0]
+    oracle.check_exact(q, x, k, v0.cpu().numpy(), i0.cpu().numpy().astype(np.int64))
+    for v, i, _ in outs[1:]:
+        np.testing.assert_allclose(v.cpu().numpy(), v0.cpu().numpy(), rtol=0, atol=2e-6)
+        same = (i == i0).cpu().numpy()
+        assert same.all() or np.abs((v - v0).cpu().numpy())[~same].max() < 2e-6
