@@ -791,8 +791,10 @@ int64_t q8_two_phase_batch(int64_t d) { return d > 384 ? 128 : 160; }
 // scan is instantiated for.
 int64_t q8_row_bytes(int64_t d) { return d <= 384 ? 384 : d <= 768 ? 768 : 1536; }
 
+// Companion layout: int8 rows [rows, dq] | block meta [nblk] float4 | max row
+// norm (16 bytes) | row order perm [rows] int32 (companion row -> corpus row).
 struct Q8Layout {
-  int64_t dq = 0, rows = 0, nblk = 0, off_meta = 0, off_xmax = 0, bytes = 0;
+  int64_t dq = 0, rows = 0, nblk = 0, off_meta = 0, off_xmax = 0, off_perm = 0, bytes = 0;
 };
 
 Q8Layout q8_layout(int64_t n, int64_t d) {
@@ -802,7 +804,8 @@ Q8Layout q8_layout(int64_t n, int64_t d) {
   L.rows = L.nblk * 64;
   L.off_meta = align_up(L.rows * L.dq, 256);
   L.off_xmax = L.off_meta + L.nblk * 16;
-  L.bytes = L.off_xmax + 16;
+  L.off_perm = align_up(L.off_xmax + 16, 256);
+  L.bytes = L.off_perm + L.rows * 4;
   return L;
 }
 
@@ -1067,6 +1070,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   fa.d = (int)d;
   fa.ntiles = P.ntiles;
   fa.tpc = P.tpc;
+  fa.perm = reinterpret_cast<const int*>(static_cast<const char*>(xq) + L.off_perm);
   if (P.gemv) {  // list L = rows [L * rows_per_wave, (L + 1) * rows_per_wave)
     fa.tile_rows = (int)P.rows_per_wave;
     fa.wave_rows = (int)P.rows_per_wave;
@@ -1128,7 +1132,8 @@ int cvs_q8_build(const void* x, int64_t n, int64_t d, void* xq, int64_t xq_bytes
   if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
   Q8BuildArgs a{static_cast<const _Float16*>(x), n, (int)d, (int)L.dq, static_cast<signed char*>(xq),
                 reinterpret_cast<float4*>(static_cast<char*>(xq) + L.off_meta),
-                reinterpret_cast<float*>(static_cast<char*>(xq) + L.off_xmax)};
+                reinterpret_cast<float*>(static_cast<char*>(xq) + L.off_xmax),
+                reinterpret_cast<int*>(static_cast<char*>(xq) + L.off_perm)};
   hipError_t e = launch_q8_build(a, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "int8 corpus build launch");
   return CVS_OK;

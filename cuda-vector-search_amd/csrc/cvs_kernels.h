@@ -137,9 +137,13 @@ struct SelectArgs {
   signed char* qq_out;
   float4* qmeta_out;
   int dq;
+  // rescore mode: list entries and list ranges are rows of the int8 companion,
+  // whose row r is corpus row perm[r] (null: the identity)
+  const int* perm;
 };
 
-// int8 companion of an fp16 corpus: rows quantised per 64-row block.
+// int8 companion of an fp16 corpus: rows ordered by their largest magnitude
+// and quantised per 64-row block.
 struct Q8BuildArgs {
   const _Float16* x;   // [n, d]
   int64_t n;
@@ -148,6 +152,7 @@ struct Q8BuildArgs {
   signed char* xq;     // [ceil(n/64)*64, dq]
   float4* bmeta;       // [ceil(n/64)]
   float* xmax;         // max over blocks of max|x_r|_2
+  int* perm;           // [ceil(n/64)*64]: companion row r holds corpus row perm[r] (r < n; perm[r] = r past n)
 };
 
 // int8 queries: per-query scale and residual norms.

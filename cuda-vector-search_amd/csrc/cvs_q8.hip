@@ -14,6 +14,15 @@
 // within that slack of A.  The kernels here store, per block, s_b and upper
 // bounds of max |f_r|_2 and max |x_r|_2 over its rows, and per query s_q,
 // |q^|_2 and |e|_2 (norms rounded up to cover fp32 accumulation).
+//
+// The companion holds the rows in ascending order of their largest magnitude
+// max_j |x_rj| (a stable sort: equal maxima keep the corpus order), so that
+// the rows sharing a block, and its scale s_b, have nearly the same maximum:
+// |f_r| then tracks each row's own scale instead of the largest of 64 random
+// rows (for unit rows of width 768, max |f_r| per block drops by ~23% and the
+// slack by ~13%).  perm[r] is the corpus row at companion row r.
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 #include "cvs_q8_row.h"
@@ -25,11 +34,41 @@ namespace {
 constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;  // > 1 + d * 2^-24 for d <= 8192, plus sqrt's ulp
 
 
-// One workgroup per 64-row block; thread t takes row t/4 and the 8-element
-// pieces p = t%4, t%4 + 4, ... of it (4 consecutive lanes read 64 contiguous
-// bytes).  Pass 1: block max |x|; pass 2 (re-reading the rows, now in cache):
-// quantise, write the int8 row and its zero padding, and reduce the row's
-// residual and value norms.
+// Sort keys: the fp16 bit pattern of max_j |x_rj| (non-negative halves order
+// like their bit patterns; NaNs are skipped as fmaxf skips them), 16 lanes per
+// row, and the row ids to carry along.
+__global__ __launch_bounds__(kBlock) void q8_rowkey_kernel(const _Float16* x, int64_t n, int d, uint16_t* key,
+                                                           int* ids) {
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+  const int l16 = threadIdx.x & 15;
+  float m = 0.f;
+  if (row < n) {
+    const half8* src = reinterpret_cast<const half8*>(x + row * (int64_t)d);
+    for (int p = l16; p < d / 8; p += 16) {
+      const half8 v = src[p];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf((float)v[j]));
+    }
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (row < n && l16 == 0) {
+    key[row] = __builtin_bit_cast(uint16_t, (_Float16)m);  // m is a half's magnitude: exact
+    ids[row] = (int)row;
+  }
+}
+
+// perm[r] = r for the padding rows r in [n, rows).
+__global__ __launch_bounds__(kBlock) void q8_perm_pad_kernel(int* perm, int64_t n, int64_t rows) {
+  const int64_t r = n + (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (r < rows) perm[r] = (int)r;
+}
+
+// One workgroup per 64-row block of the companion; thread t takes companion
+// row t/4 (corpus row perm[t/4]) and the 8-element pieces p = t%4, t%4 + 4,
+// ... of it (4 consecutive lanes read 64 contiguous bytes).  Pass 1: block max
+// |x|; pass 2 (re-reading the rows, now in cache): quantise, write the int8 row
+// and its zero padding, and reduce the row's residual and value norms.
 __global__ __launch_bounds__(kBlock) void q8_build_kernel(Q8BuildArgs a) {
   __shared__ float red[kBlock / kWave];
   __shared__ float fmax_s[kBlock / kWave], xmax_s[kBlock / kWave];
@@ -41,7 +80,8 @@ __global__ __launch_bounds__(kBlock) void q8_build_kernel(Q8BuildArgs a) {
   const int part = tid & 3;
   const bool live = row < a.n;
   const int pieces = a.d / 8;  // 8-element pieces per row
-  const half8* src = reinterpret_cast<const half8*>(a.x + (live ? row : 0) * (int64_t)a.d);
+  const int64_t srow = live ? a.perm[row] : 0;
+  const half8* src = reinterpret_cast<const half8*>(a.x + srow * (int64_t)a.d);
 
   float m = 0.f;
   if (live) {
@@ -128,10 +168,38 @@ __global__ __launch_bounds__(kBlock) void q8_query_kernel(Q8QueryArgs a) {
 
 }  // namespace
 
+// Row order, then the blocks.  The sort's key and id buffers and its scratch
+// are one stream-ordered allocation, released on the stream after the sort.
 hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
-  if (a.d < 8 || a.d % 8 != 0 || a.dq < a.d || a.dq % 128 != 0) return hipErrorInvalidValue;
+  if (a.d < 8 || a.d % 8 != 0 || a.dq < a.d || a.dq % 128 != 0 || a.perm == nullptr) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + 63) / 64;
-  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  if (blocks <= 0 || blocks > 0x7fffffff || a.n >= 0x7fffffff) return hipErrorInvalidValue;
+  const int64_t n = a.n, rows = blocks * 64;
+  size_t sort_bytes = 0;
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_bytes, (const uint16_t*)nullptr, (uint16_t*)nullptr,
+                                           (const int*)nullptr, (int*)nullptr, (unsigned)n, 0, 15, s);
+  if (e != hipSuccess) return e;
+  const size_t keys_bytes = ((size_t)n * sizeof(uint16_t) + 255) / 256 * 256;
+  const size_t ids_bytes = ((size_t)n * sizeof(int) + 255) / 256 * 256;
+  char* buf = nullptr;
+  e = hipMallocAsync(reinterpret_cast<void**>(&buf), 2 * keys_bytes + ids_bytes + sort_bytes, s);
+  if (e != hipSuccess) return e;
+  uint16_t* key_in = reinterpret_cast<uint16_t*>(buf);
+  uint16_t* key_out = reinterpret_cast<uint16_t*>(buf + keys_bytes);
+  int* ids = reinterpret_cast<int*>(buf + 2 * keys_bytes);
+  void* tmp = buf + 2 * keys_bytes + ids_bytes;
+  const int per = kBlock / 16;
+  hipLaunchKernelGGL(q8_rowkey_kernel, dim3((unsigned)((n + per - 1) / per)), dim3(kBlock), 0, s, a.x, n, a.d,
+                     key_in, ids);
+  e = hipGetLastError();
+  if (e == hipSuccess)
+    e = rocprim::radix_sort_pairs(tmp, sort_bytes, key_in, key_out, ids, a.perm, (unsigned)n, 0, 15, s);
+  const hipError_t ef = hipFreeAsync(buf, s);
+  if (e != hipSuccess) return e;
+  if (ef != hipSuccess) return ef;
+  if (rows > n)
+    hipLaunchKernelGGL(q8_perm_pad_kernel, dim3((unsigned)((rows - n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s,
+                       a.perm, n, rows);
   hipLaunchKernelGGL(q8_build_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
   hipLaunchKernelGGL(q8_xmax_kernel, dim3(1), dim3(kBlock), 0, s, a.bmeta, blocks, a.xmax);
   return hipGetLastError();

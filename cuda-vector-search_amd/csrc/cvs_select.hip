@@ -685,9 +685,14 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
       }
     }
 #pragma unroll
+    for (int j = 0; j < kGather; ++j) {  // companion rows -> corpus rows
+      if (idv[j] < 0 || idv[j] >= a.n) idv[j] = -1;
+      else if (a.perm) idv[j] = a.perm[idv[j]];
+    }
+#pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const uint64_t key = make_key(val[j], idv[j]);
-      if (idv[j] >= 0 && idv[j] < a.n && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+      if (idv[j] >= 0 && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
     }
     const bool last = base + kBatch >= total;
     if (a.exact) {
@@ -746,10 +751,14 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
     if (tid == 0) nrows = 0;
     __syncthreads();
     int idv[kGather];
+    float uv[kGather];
+    bool fromlist[kGather];
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {  // lookups and loads first (see select_kernel)
       const int gi = base + j * kBlock + tid;
       idv[j] = -1;
+      uv[j] = 0.f;
+      fromlist[j] = false;
       if (gi < total) {
         const int L = list_of(S, NL, gi);
         const int idx = gi - S.pre[L];
@@ -760,10 +769,18 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
         } else if (!a.exact) {
           const int64_t off = ((int64_t)q * NL + L) * a.cap + idx;
           const int lid = a.li[off];
-          const float u = a.lv[off];
-          if (lid >= 0 && lid < a.n && make_key(u, lid) < ucut && u >= umin) idv[j] = lid;
+          uv[j] = a.lv[off];
+          if (lid >= 0 && lid < a.n && uv[j] >= umin) {
+            idv[j] = lid;
+            fromlist[j] = true;
+          }
         }
       }
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {  // companion rows -> corpus rows; list entries phase 1 kept are out
+      if (idv[j] >= 0 && a.perm) idv[j] = a.perm[idv[j]];
+      if (fromlist[j] && make_key(uv[j], idv[j]) >= ucut) idv[j] = -1;
     }
 #pragma unroll
     for (int j = 0; j < kGather; ++j)
@@ -789,7 +806,8 @@ __global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
   __shared__ int pre[kBlock + 1];
   __shared__ int wsum[kWaves];
   __shared__ int kept[kBlock];      // survivors per list so far
-  __shared__ int sid[kBatch];       // a batch's candidate ids
+  __shared__ int sid[kBatch];       // a batch's candidates (companion rows, as listed)
+  __shared__ int sxr[kBatch];       // ... their corpus rows
   __shared__ short slist[kBatch];   // ... and their lists (local index)
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -854,23 +872,33 @@ __global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
         lov[j] = lo;
       }
     }
+    int xrv[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      if (idv[j] < 0 || idv[j] >= a.n) idv[j] = -1;
+      xrv[j] = (idv[j] >= 0 && a.perm) ? a.perm[idv[j]] : idv[j];
+    }
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const int i = j * kBlock + tid;
       if (i < cnt) {
-        sid[i] = (idv[j] >= 0 && idv[j] < a.n) ? idv[j] : -1;
+        sid[i] = idv[j];
+        sxr[i] = xrv[j];
         slist[i] = (short)lov[j];
       }
     }
     __syncthreads();
     for (int c0 = (tid >> 4) * RU; c0 < cnt; c0 += (kBlock / 16) * RU) {
-      int idu[RU];
+      int idu[RU], xru[RU];
       half8 xv[RU][RL];
 #pragma unroll
-      for (int u = 0; u < RU; ++u) idu[u] = c0 + u < cnt ? sid[c0 + u] : -1;
+      for (int u = 0; u < RU; ++u) {
+        idu[u] = c0 + u < cnt ? sid[c0 + u] : -1;
+        xru[u] = c0 + u < cnt ? sxr[c0 + u] : -1;
+      }
 #pragma unroll
       for (int u = 0; u < RU; ++u) {
-        const half8* xr = reinterpret_cast<const half8*>(a.x + (int64_t)(idu[u] < 0 ? 0 : idu[u]) * a.d);
+        const half8* xr = reinterpret_cast<const half8*>(a.x + (int64_t)(idu[u] < 0 ? 0 : xru[u]) * a.d);
 #pragma unroll
         for (int m = 0; m < RL; ++m) {
           const int cc = l16 + 16 * m;

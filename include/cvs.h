@@ -187,10 +187,14 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
  *
  * cvs_q8_corpus_bytes: size of the companion of an [n, d] corpus (int8 rows of
  *   384, 768 or 1536 bytes, the smallest that holds d, plus 16 bytes per
- *   64-row block and 16 bytes for the corpus-wide maximum row norm).
+ *   64-row block, 16 bytes for the corpus-wide maximum row norm and 4 bytes
+ *   per row for the row order).
  * cvs_q8_build: writes the companion of x (d multiple of 64, <= 1536) into xq
- *   (256-byte aligned, at least cvs_q8_corpus_bytes).  Rebuild it whenever x
- *   changes.
+ *   (256-byte aligned, at least cvs_q8_corpus_bytes): the rows in ascending
+ *   order of their largest magnitude (stable), so that each 64-row block, which
+ *   shares one int8 scale, holds rows of nearly equal range.  Rebuild it
+ *   whenever x changes.  The call allocates (and releases, stream-ordered) a
+ *   scratch buffer of about 8 bytes per row for the sort.
  * cvs_q8_plan / cvs_q8_topk: as cvs_fused_plan / cvs_fused_topk (1 <= k <= 256,
  *   auto plan only; flags CVS_FLAG_IDS_INT64, and the pre-pass flags for the
  *   sampling pass), with the companion of x as xq.  plan_out[0] is the int8

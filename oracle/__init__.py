@@ -19,12 +19,15 @@ Contents, each restating one reference function (file:line into the reference):
   argpartition + argsort), used as a CPU baseline.
 * ``normalize_rows``     - ``index.py:35-41`` + ``index.py:27-32`` (cosine
   normalisation and zero-padding of fp16 rows).
-* ``q8_quantize_blocks`` / ``q8_quantize_queries`` / ``q8_bound`` - the int8
-  pre-filter's data format (this build's own design; no reference counterpart):
-  symmetric int8 rows with one scale per 64-row corpus block or per query, and
-  the Cauchy-Schwarz bound |q.x - A| <= |q^| |f| + |e| |x| that keeps the
-  pre-filter exact.  Pinned by closed forms (scales, saturation, ties-to-even)
-  and by the bound holding, and failing without either term, on random data.
+* ``q8_row_order`` / ``q8_quantize_blocks`` / ``q8_companion`` /
+  ``q8_quantize_queries`` / ``q8_bound`` - the int8 pre-filter's data format
+  (this build's own design; no reference counterpart): corpus rows in
+  ascending order of their largest magnitude (stable), symmetric int8 rows
+  with one scale per 64-row block of that order or per query, and the
+  Cauchy-Schwarz bound |q.x - A| <= |q^| |f| + |e| |x| that keeps the
+  pre-filter exact.  Pinned by closed forms (scales, saturation, ties-to-even,
+  the order of rows with planted maxima, stability of equal maxima) and by the
+  bound holding, and failing without either term, on random data.
 * ``check_exact``        - the acceptance rule of ``tests/test_search.py:21-44``
   plus the id-parity rule (ids identical except inside the near-tie band of the
   k-th score).
@@ -221,8 +224,21 @@ def _q8_rows(f32: np.ndarray):
     return qv.astype(np.float64), s
 
 
-def q8_quantize_blocks(x, block: int = 64):
-    """int8 companion of an fp16 corpus (``cvs_q8.hip`` ``q8_build_kernel``).
+def q8_row_order(x) -> np.ndarray:
+    """Row order of the int8 companion (``cvs_q8.hip`` ``q8_rowkey_kernel`` and
+    its stable radix sort): corpus rows by ascending max_j |x_rj| compared as
+    fp16 bit patterns (NaNs skipped, an all-NaN row counts as 0), equal maxima
+    in corpus order.  Entry c is the corpus row at companion row c."""
+    x16 = _as_half(x)
+    m = np.fmax.reduce(np.abs(x16), axis=1, initial=np.float16(0)) if x16.size else \
+        np.zeros(x16.shape[0], dtype=np.float16)
+    return np.argsort(m.astype(np.float16).view(np.uint16), kind="stable")
+
+
+def q8_quantize_blocks(x, block: int = 64, order=None):
+    """int8 companion rows of an fp16 corpus (``cvs_q8.hip`` ``q8_build_kernel``),
+    taking the rows in ``order`` (companion row c = corpus row order[c]; None:
+    corpus order).
 
     Returns ``(xq, meta)``: ``xq`` int8 ``[ceil(n/64)*64, q8_row_bytes(d)]`` (zero
     padding columns and rows) and ``meta`` float64 ``[ceil(n/64), 3]`` = (block
@@ -230,6 +246,8 @@ def q8_quantize_blocks(x, block: int = 64):
     max_r |x_r|_2) with f_r = x_r - s_b x~_r.  The GPU stores the two norms
     rounded up; a test checks they are >= these and within 0.2%."""
     x16 = _as_half(x)
+    if order is not None:
+        x16 = x16[np.asarray(order)]
     n, d = x16.shape
     dq = q8_row_bytes(d)
     nblk = -(-n // block)
@@ -245,6 +263,18 @@ def q8_quantize_blocks(x, block: int = 64):
         meta[b, 1] = np.sqrt((f * f).sum(axis=1)).max()
         meta[b, 2] = np.sqrt((rows.astype(np.float64) ** 2).sum(axis=1)).max()
     return xq, meta
+
+
+def q8_companion(x, block: int = 64):
+    """The whole int8 companion as ``cvs_q8_build`` writes it: ``(xq, meta,
+    perm)`` with the rows in ``q8_row_order`` and ``perm`` int32
+    ``[ceil(n/64)*64]`` (companion row -> corpus row; padding rows map to
+    themselves)."""
+    order = q8_row_order(x)
+    xq, meta = q8_quantize_blocks(x, block, order)
+    perm = np.arange(xq.shape[0], dtype=np.int32)
+    perm[:order.size] = order
+    return xq, meta, perm
 
 
 def q8_quantize_queries(q):
@@ -265,17 +295,19 @@ def q8_quantize_queries(q):
     return qq, meta
 
 
-def q8_bound(q, x, block: int = 64):
+def q8_bound(q, x, block: int = 64, order=None):
     """(A, B, S): the int8 estimate A = s_q s_b sum(q~ x~), the bound B =
     |q^| |f_r| + |e| |x_r| (per row, exact), and the exact scores S = q.x in
-    float64, for every (query, row) pair."""
+    float64, for every (query, corpus row) pair, with the blocks formed over
+    the rows in ``order`` (as ``q8_quantize_blocks``)."""
     x16, q16 = _as_half(x), _as_half(q)
     n, d = x16.shape
-    xq, _ = q8_quantize_blocks(x16, block)
+    xq, meta = q8_quantize_blocks(x16, block, order)
     qq, qm = q8_quantize_queries(q16)
-    xs = np.repeat(q8_quantize_blocks(x16, block)[1][:, 0], block)[:n]
+    pos = np.arange(n) if order is None else np.argsort(np.asarray(order))  # companion row of each corpus row
+    xs = np.repeat(meta[:, 0], block)[pos]
     xf = x16.astype(np.float64)
-    xt = xq[:n, :d].astype(np.float64)
+    xt = xq[pos, :d].astype(np.float64)
     A = (qq[:, :d].astype(np.float64) @ xt.T) * qm[:, :1] * xs[None, :]
     f = xf - xs[:, None] * xt
     B = qm[:, 1:2] * np.sqrt((f * f).sum(axis=1))[None, :] + qm[:, 2:3] * np.sqrt((xf * xf).sum(axis=1))[None, :]

@@ -542,10 +542,11 @@ def test_q8_build_matches_oracle(eng, n, d):
     say(f"q8 build n={n} d={d}")
     rng = np.random.default_rng(n + d)
     x = (rng.standard_normal((n, d)) * rng.uniform(0.01, 2, (n, 1))).astype(np.float16)
+    x[n // 3:n // 3 + min(70, n // 2)] = x[5]  # equal maxima, across a block boundary: stable order
     xd = pad64(torch.from_numpy(x)).cuda().contiguous()
     xq = eng.q8_build(xd)
     torch.cuda.synchronize()
-    ref_q, ref_m = oracle.q8_quantize_blocks(xd.cpu().numpy())
+    ref_q, ref_m, ref_p = oracle.q8_companion(xd.cpu().numpy())
     raw = xq.cpu().numpy()
     body = raw[:ref_q.size].view(np.int8).reshape(ref_q.shape)
     assert np.array_equal(body, ref_q)
@@ -557,7 +558,10 @@ def test_q8_build_matches_oracle(eng, n, d):
         assert (meta[:, j] >= ref_m[:, j]).all()
         assert (meta[:, j] <= ref_m[:, j] * 1.002 + 1e-30).all()
     xmax = raw[off + 16 * nblk:off + 16 * nblk + 4].view(np.float32)[0]
-    assert xmax == meta[:, 2].max() and raw.size == off + 16 * nblk + 16
+    assert xmax == meta[:, 2].max()
+    off_perm = -(-(off + 16 * nblk + 16) // 256) * 256
+    perm = raw[off_perm:off_perm + 4 * ref_p.size].view(np.int32)
+    assert np.array_equal(perm, ref_p) and raw.size == off_perm + 4 * ref_p.size
 
 
 Q8_CASES = [(1, 30000, 384, 10), (7, 20000, 320, 5), (33, 25000, 384, 64), (65, 30000, 512, 10),
@@ -616,8 +620,10 @@ def test_q8_overflowing_lists_are_rescanned(eng):
 @pytest.mark.gpu
 @pytest.mark.parametrize("nq,k", [(1, 10), (64, 100), (160, 10), (160, 100)])
 def test_q8_loose_bounds_reorder_candidates(eng, nq, k):
-    """Blocks holding one very long row get a coarse int8 scale, so their other
-    rows carry score bounds near 1 while their exact scores are ordinary: the k
+    """A block holding a very long row gets a coarse int8 scale, so its other
+    rows carry score bounds near 1 while their exact scores are ordinary (the
+    companion orders rows by their largest magnitude: the five long rows share
+    the last block with the 59 ordinary rows of largest magnitude): the k
     candidates of largest bound, which the select rescores first, are not the
     top k, and the exact result has to come from the remaining candidates.
     Batches below 128 rescore every candidate before the select; from 128 on
@@ -642,23 +648,32 @@ def test_q8_loose_bounds_reorder_candidates(eng, nq, k):
     say(f"  id mismatches {int((~same).sum())}")
     assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
     assert oracle.check_exact(q.numpy(), x.numpy(), k, v8, i8) >= 0.99
-    # the loose blocks' ordinary rows are not what the search returns
-    loose = {blk * 64 + r for blk in (10, 150, 300, 450, 600) for r in range(1, 64)}
+    # the loose block's ordinary rows are not what the search returns
+    order = oracle.q8_row_order(pad64(x).numpy())
+    spikes = {blk * 64 for blk in (10, 150, 300, 450, 600)}
+    assert set(order[-5:].tolist()) == spikes
+    loose = set(order[-64:-5].tolist())
     assert np.isin(i8, list(loose)).mean() < 0.2
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("k", [10, 100])
 def test_q8_equal_bounds_fall_back_to_the_exact_cut(eng, k):
-    """Six 64-row blocks made of copies of query 0's row, far apart: 384
-    candidates in ordinary lists (none overflows) share one score bound, so the
-    select's histogram cut cannot isolate k of them and takes the exact cut;
-    the result is the k copies of smallest id."""
+    """Six 64-row runs of copies of one row close to query 0, far apart in the
+    corpus; its largest magnitude (0.9) exceeds every other row's, so the
+    companion's row order puts the 384 copies into its last six blocks, with
+    equal block metadata: 384 candidates in ordinary lists (none overflows)
+    share one score bound, so the select's histogram cut cannot isolate k of
+    them and takes the exact cut; the result is the k copies of smallest id."""
     say(f"q8 equal bounds k={k}")
     x, q = make(40000, 384, 160, seed=23 + k)
+    row = q[0].clone()
+    j = int(row.abs().argmax())
+    row[j] = 0.9 if row[j] > 0 else -0.9
+    assert float(x.abs().max()) < 0.9
     blocks = (20, 140, 260, 380, 500, 620)
     for blk in blocks:
-        x[blk * 64:(blk + 1) * 64] = q[0]
+        x[blk * 64:(blk + 1) * 64] = row
     qd = pad64(q).cuda().contiguous()
     xd = pad64(x).cuda().contiguous()
     xq = eng.q8_build(xd)

@@ -258,6 +258,52 @@ def test_q8_quantisation_closed_forms():
     assert np.isclose(qm[1, 0], np.float32(np.float32(0.5) / np.float32(127)))
 
 
+def test_q8_row_order_closed_forms():
+    # planted row maxima: ascending order of max |x_r|, negatives by magnitude
+    x = np.zeros((6, 64), dtype=np.float16)
+    x[0, 3] = 5.0
+    x[1, 0] = -0.25
+    x[2, 7] = 2.0
+    x[3, 1] = -9.0
+    x[4, 2] = 0.5
+    x[4, 5] = -0.75       # max |x| 0.75
+    # row 5: all zero (max 0)
+    assert oracle.q8_row_order(x).tolist() == [5, 1, 4, 2, 0, 3]
+    # equal maxima keep the corpus order (stable), also among copies
+    y = np.zeros((7, 64), dtype=np.float16)
+    y[:, 0] = [3, 1, 3, -1, 2, 3, 1]
+    assert oracle.q8_row_order(y).tolist() == [1, 3, 6, 4, 0, 2, 5]
+    # NaNs are skipped; an all-NaN row counts as 0
+    z = np.ones((3, 64), dtype=np.float16)
+    z[0, 5] = np.nan
+    z[1, :] = np.nan
+    z[2, 9] = 4
+    assert oracle.q8_row_order(z).tolist() == [1, 0, 2]
+
+
+def test_q8_companion_layout_and_order_invariants():
+    rng = np.random.default_rng(9)
+    n, d = 300, 128
+    x = (rng.standard_normal((n, d)) * rng.uniform(0.1, 3, (n, 1))).astype(np.float16)
+    x[40:60] = x[10]      # equal maxima
+    xq, meta, perm = oracle.q8_companion(x)
+    rows = -(-n // 64) * 64
+    assert perm.dtype == np.int32 and perm.shape == (rows,)
+    assert sorted(perm[:n].tolist()) == list(range(n))            # a permutation
+    assert perm[n:].tolist() == list(range(n, rows))              # padding maps to itself
+    mx = np.abs(x.astype(np.float32)).max(axis=1)
+    assert (np.diff(mx[perm[:n]]) >= 0).all()                     # ascending maxima
+    same = [c for c in range(n) if mx[perm[c]] == mx[10]]
+    assert perm[same].tolist() == sorted(perm[same].tolist())      # stable among equals
+    # the companion's rows are the corpus rows in that order, block-quantised
+    xq2, meta2 = oracle.q8_quantize_blocks(x[perm[:n]])
+    assert np.array_equal(xq, xq2) and np.array_equal(meta, meta2)
+    # ordered blocks share their scale with rows of nearly the same maximum:
+    # every block's scale is at most that of the same rows in corpus order
+    _, meta_c = oracle.q8_quantize_blocks(x)
+    assert meta[:, 0].sum() < meta_c[:, 0].sum()
+
+
 def test_q8_bound_holds_and_needs_both_terms():
     rng = np.random.default_rng(5)
     # random rows of mixed scales, including heavy-tailed ones
@@ -266,6 +312,10 @@ def test_q8_bound_holds_and_needs_both_terms():
     q = rng.standard_normal((9, 384)).astype(np.float16)
     A, B, S = oracle.q8_bound(q, x)
     assert (np.abs(S - A) <= B).all()
+    # ... and over the blocks of the companion's row order, where it is tighter
+    A2, B2, S2 = oracle.q8_bound(q, x, order=oracle.q8_row_order(x))
+    assert np.array_equal(S2, S) and (np.abs(S2 - A2) <= B2).all()
+    assert B2.mean() < B.mean()
     # a query that is exactly representable (integers, max 127: e = 0) and
     # aligned with a row's residual f: |S - A| = |q.f| reaches |q^||f|, so the
     # bound without its f-term (|e||x| = 0) fails
