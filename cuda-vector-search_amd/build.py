@@ -42,12 +42,13 @@ FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-SOURCES = ["cvs_scan.hip", "cvs_select.hip", "cvs_gemv.hip", "cvs_prep.hip", "cvs_q8.hip", "cvs_capi.hip"]
+SOURCES = ["cvs_scan.hip", "cvs_scan_q8.hip", "cvs_select.hip", "cvs_gemv.hip", "cvs_prep.hip", "cvs_q8.hip", "cvs_capi.hip"]
 
 # Per-source extra flags.  The scan keeps its MFMA accumulators in VGPRs (the
 # query fragments are pinned in AGPRs explicitly): the epilogue then reads the
 # scores without 64 v_accvgpr_read per tile (measured 3-6% faster scan).
-EXTRA = {"cvs_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+MFMA_SOURCES = ["cvs_scan.hip", "cvs_scan_q8.hip"]  # kernels whose MFMA results the build checks
+EXTRA = {"cvs_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "cvs_scan_q8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd, verbose):
@@ -80,12 +81,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         objs.append(obj)
         cmds.append([HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", CSRC / src, "-o", obj])
     # device assembly of the MFMA kernels, for the result-hazard check below
-    asm = BUILD / "cvs_scan.s"
-    cmds.append([HIPCC, *FLAGS, *EXTRA["cvs_scan.hip"], "--cuda-device-only", "-S", "-c", CSRC / "cvs_scan.hip",
-                 "-o", asm])
+    asms = []
+    for src in MFMA_SOURCES:
+        asm = BUILD / (Path(src).stem + ".s")
+        asms.append(asm)
+        cmds.append([HIPCC, *FLAGS, *EXTRA[src], "--cuda-device-only", "-S", "-c", CSRC / src, "-o", asm])
     with ThreadPoolExecutor(max_workers=jobs or min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    early = hazard_check.check(asm)
+    early = [p for asm in asms for p in hazard_check.check(asm)]
     if early:
         raise RuntimeError(f"{len(early)} MFMA results read too early in the scan kernels, e.g. " + early[0])
     tmp = LIB.with_suffix(".so.tmp")

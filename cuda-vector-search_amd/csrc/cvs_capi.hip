@@ -1050,7 +1050,11 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     a.qmeta = qm;
     a.bmeta = bmeta;
     a.gamma = gamma;
-    e = launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
+    const ScanCfg c384{32, 8, 1, 2, 12};
+    const bool lean = P.cfg.ms == c384.ms && P.cfg.qs == c384.qs && P.cfg.qb == c384.qb && P.cfg.rb == c384.rb &&
+                      P.cfg.ksmax == c384.ksmax && q8scan384_fits(a);
+    e = lean ? launch_q8scan384(a, (int)(P.groups * P.chunks), s)
+             : launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
     if (e != hipSuccess) return hip_fail(e, "int8 scan launch");
   }
   mark(3);

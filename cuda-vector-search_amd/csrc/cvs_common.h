@@ -103,6 +103,39 @@ __device__ __forceinline__ half8 pin_agpr(half8 v) {
   return r;
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 pin_agpr(i32x4 v) {
+  i32x4 r = v;
+  asm volatile("" : "+a"(r));
+  return r;
+}
+
+// ---- MFMA scan helpers --------------------------------------------------------
+
+// Wait states between a tile's last MFMA and the epilogue's first VALU read of
+// its accumulators.  gfx950 needs passes + 4 for a VALU read of an MFMA's VGPR
+// result; with the accumulators in VGPRs (-amdgpu-mfma-vgpr-form) this
+// compiler leaves only passes + 3 between them, and the epilogue then reads a
+// partial sum (the score matrix intermittently lacked the last k-step).  The
+// pad is 2 * passes + 3, tied to the accumulator so that it follows the last
+// MFMA; the build checks every MFMA result read of the scan kernels against
+// passes + 4 (hazard_check.py).
+template <int PASSES, class T>
+__device__ __forceinline__ void pad_mfma_result(T& acc) {
+  constexpr int WS = 2 * PASSES + 3;
+  static_assert(WS > 8 && WS <= 24, "pad of 9..24 wait states");
+  if constexpr (WS > 16)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 17));
+  else
+    asm volatile("s_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 9));
+}
+
+// Piece permutation of corpus stages in LDS: slot s of a stage row R holds
+// 16-byte piece s ^ piece_swz(R), so the 8 (and 16) consecutive rows whose
+// equal-index pieces one MFMA fragment's lanes read fall on distinct banks.
+__device__ __forceinline__ int piece_swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
 // ---- wave utilities ---------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }

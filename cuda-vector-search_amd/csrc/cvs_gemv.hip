@@ -23,8 +23,6 @@ namespace {
 
 constexpr int kUnr = 2;  // 8-row groups per wave per iteration
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
 // 16 int8 x 16 int8, exact.
 __device__ __forceinline__ int dot16_i8(half8 a, half8 b, int acc) {
   const i32x4 x = __builtin_bit_cast(i32x4, a), y = __builtin_bit_cast(i32x4, b);

@@ -185,6 +185,10 @@ struct ScanCfg {
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
+// int8 scan of 384-byte rows at 256 queries per workgroup (cfg {32, 8, 1, 2, 12}):
+// the same lists as launch_scan(cfg, kAppendQ8, ...), from a leaner kernel.
+bool q8scan384_fits(const ScanArgs& a);
+hipError_t launch_q8scan384(const ScanArgs& a, int grid, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs& a, int grid, hipStream_t s);  // any d % 64 == 0 (int8: 384/768/1536 bytes)
 hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);  // 0 final, 1 threshold, 2 rescore
 hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);

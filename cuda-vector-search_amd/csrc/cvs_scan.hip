@@ -76,7 +76,6 @@ struct Mfma<32> {
 // lane as for 32x32x16_f16 (lane l: row l%32, bytes 16(l/32)..+15 of a 32-byte
 // k-step), so the kernel's byte addressing is unchanged: it runs on int8 rows
 // with d counted in 2-byte units.  Same D layout as Mfma<32>.
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 struct MfmaI8 {
   typedef int acc_t __attribute__((ext_vector_type(16)));
   static constexpr int KSZ = 16;  // 2-byte units per k-step (32 int8)
@@ -98,24 +97,6 @@ struct MfmaFor<32, kAppendQ8> {
   typedef MfmaI8 type;
 };
 
-// Wait states between a tile's last MFMA and the epilogue's first VALU read of
-// its accumulators.  gfx950 needs passes + 4 for a VALU read of an MFMA's VGPR
-// result; with the accumulators in VGPRs (-amdgpu-mfma-vgpr-form) this
-// compiler leaves only passes + 3 between them, and the epilogue then reads a
-// partial sum (the score matrix intermittently lacked the last k-step).  The
-// pad is 2 * passes + 3, tied to the accumulator so that it follows the last
-// MFMA; the build checks every MFMA result read of the scan kernels against
-// passes + 4 (hazard_check.py).
-template <int PASSES, class T>
-__device__ __forceinline__ void pad_mfma_result(T& acc) {
-  constexpr int WS = 2 * PASSES + 3;
-  static_assert(WS > 8 && WS <= 24, "pad of 9..24 wait states");
-  if constexpr (WS > 16)
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 17));
-  else
-    asm volatile("s_nop 7\n\ts_nop %1" : "+v"(acc) : "n"(WS - 9));
-}
-
 // FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
 // compile-time constant (per-stage guards on a runtime count split the
 // unrolled stage loop into separate blocks and cost ~15% of the scan).
@@ -124,7 +105,6 @@ __device__ __forceinline__ void pad_mfma_result(T& acc) {
 // so every load reads 8 whole 128-byte lines.  Slot s of row R holds piece
 // s ^ piece_swz(R): the 8 (and 16) consecutive rows whose equal-index pieces
 // the lanes of one fragment read then fall on distinct LDS banks.
-__device__ __forceinline__ int piece_swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
 __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArgs a) {
