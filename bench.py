@@ -192,7 +192,7 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
 
 # Demangled names of the dominant kernel's dispatches (mode 0 = candidate append).
 DOMINANT = {"scan": re.compile(r"scan_kernel<(?:\d+,\s*){5}0\b"), "gemv": re.compile(r"gemv_kernel<\d+,\s*0>"),
-            "scan_q8": re.compile(r"scan_kernel<(?:\d+,\s*){5}4\b"),
+            "scan_q8": re.compile(r"scan_kernel<(?:\d+,\s*){5}4\b|q8scan384_kernel"),
             "gemv_q8": re.compile(r"gemv_kernel<\d+,\s*4>")}
 COPY_KERNEL = re.compile(r"copyBuffer")  # torch copy_ between device tensors = hipMemcpyAsync
 COPY_BYTES = 1 << 30

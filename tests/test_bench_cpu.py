@@ -24,6 +24,7 @@ def test_dominant_kernel_patterns_match_the_append_launches_only():
     assert bench.COPY_KERNEL.search("__amd_rocclr_copyBuffer")
     scan8 = bench.DOMINANT["scan_q8"]
     assert scan8.search("void cvs::(anonymous namespace)::scan_kernel<32, 8, 1, 2, 12, 4, true>(cvs::ScanArgs)")
+    assert scan8.search("cvs::(anonymous namespace)::q8scan384_kernel(cvs::ScanArgs)")
     assert not scan8.search("void cvs::(anonymous namespace)::scan_kernel<32, 8, 1, 2, 24, 1, true>(cvs::ScanArgs)")
     gemv8 = bench.DOMINANT["gemv_q8"]
     assert gemv8.search("void cvs::(anonymous namespace)::gemv_kernel<6, 4>(cvs::GemvArgs)")
@@ -40,6 +41,8 @@ def test_dominant_kernel_follows_the_auto_path():
 def test_instantiated_kernels_are_the_ones_the_patterns_expect():
     src = (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_scan.hip").read_text()
     assert "template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>" in src
+    lean = (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_scan_q8.hip").read_text()
+    assert "void q8scan384_kernel(ScanArgs a)" in lean
     hdr = (REPO / "cuda-vector-search_amd" / "csrc" / "cvs_kernels.h").read_text()
     assert "kAppend = 0," in hdr and "kAppendQ8 = 4," in hdr
 
