@@ -527,12 +527,19 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
 }
 
+// The threshold kernels stop their bit search above the kTauLowBits low bits
+// of the 32-bit order key: the result, the largest key t with #(keys >= t) >= k
+// among keys whose low bits are zero, is at most the exact k-th largest key
+// (so still a valid filter: a lower bound on the k-th best score) and below
+// it by less than 2^kTauLowBits order steps, about 2^-11 of the score.
+constexpr int kTauLowBits = 12;
+
 // Threshold mode with few units (<= 64 U per query, the sampling pre-pass's
 // maxima in one list of `cap` floats): one wave per query.  The k-th largest
 // score is found as the largest 32-bit order key t with #(keys >= t) >= k, bit
-// by bit from the most significant, each count a ballot per register and a
-// scalar popcount (no cross-lane shuffles); it is the same score the general
-// select returns.  The int8 pre-filter's query quantisation rides along.
+// by bit from the most significant down to kTauLowBits, each count a ballot per
+// register and a scalar popcount (no cross-lane shuffles).  The int8
+// pre-filter's query quantisation rides along.
 template <int U>
 __global__ __launch_bounds__(kWave) void tau_kernel(SelectArgs a) {
   const int q = blockIdx.x;
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(kWave) void tau_kernel(SelectArgs a) {
   uint32_t t = 0;
   if (m >= a.k) {
 #pragma unroll 1
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= kTauLowBits; --bit) {
       const uint32_t cand = t | (1u << bit);
       int c = 0;
 #pragma unroll
@@ -563,6 +570,52 @@ __global__ __launch_bounds__(kWave) void tau_kernel(SelectArgs a) {
   }
   if (lane == 0) a.tau[q] = (m >= a.k) ? order_float(t) : -__builtin_inff();
   if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane);
+}
+
+// Threshold mode with up to U * 256 units per query (one list, as tau_kernel
+// takes): the same bit-by-bit search over one 256-thread workgroup, each
+// thread holding U keys; a bit's count is the four waves' ballot counts summed
+// in LDS.  The count buffers alternate by bit, so one barrier per bit suffices:
+// a wave writes buffer b & 1 again only after the barrier of bit b - 1, which
+// every wave reaches after reading bit b's counts.  Wave 0 quantises the query
+// for the int8 pre-filter as tau_kernel does.
+template <int U>
+__global__ __launch_bounds__(kBlock) void tau_block_kernel(SelectArgs a) {
+  __shared__ int cnt[2][kWaves];
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int w = tid / kWave;
+  const int m = a.cap;
+  const float* src = a.lv + (int64_t)q * m;
+  uint32_t key[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = u * kBlock + tid;
+    key[u] = i < m ? float_order(src[i]) : 0u;
+  }
+  uint32_t t = 0;
+  if (m >= a.k) {
+#pragma unroll 1
+    for (int bit = 31; bit >= kTauLowBits; --bit) {
+      const uint32_t cand = t | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) c += __popcll(__ballot(key[u] >= cand));
+      if (lane == 0) cnt[bit & 1][w] = c;
+      __syncthreads();
+      int tot = 0;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) tot += cnt[bit & 1][i];
+      if (tot >= a.k) t = cand;
+    }
+  }
+  if (tid == 0) a.tau[q] = (m >= a.k) ? order_float(t) : -__builtin_inff();
+  if (a.qq_out != nullptr && w == 0) {
+    float qrow[kQ8RowPer];
+    q8_load_row(a.q + (int64_t)q * a.d, a.d, lane, qrow);
+    q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane);
+  }
 }
 
 // Rescoring: 16 lanes per candidate row, lane l taking the row's 16-byte pieces
@@ -1030,9 +1083,15 @@ hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
         return hipErrorInvalidValue;
       if (a.nlists == 1 && a.li == nullptr && a.lcount == nullptr && a.cap >= 1 && a.cap <= 8 * kWave) {
         // one list of at most 512 unit maxima per query: the one-wave kernel
-        // (measured 6.8 vs 10.8 us at C2; with more units, or a single query,
-        // the 256-thread select is faster: 3840 units at C4, 1024 at C3)
+        // (measured 6.8 vs 10.8 us at C2 against the 256-thread select)
         hipLaunchKernelGGL(tau_kernel<8>, dim3(nq), dim3(kWave), 0, s, a);
+        break;
+      }
+      if (a.nlists == 1 && a.li == nullptr && a.lcount == nullptr && a.cap > 8 * kBlock && a.cap <= 16 * kBlock) {
+        // 2049-4096 unit maxima (k = 100 over 1M rows: 3840): the same search
+        // over a workgroup (measured 20.8 vs 23.5 us at 1M x 768, batch 256;
+        // the 256-thread select stays faster at 1024 units and one query)
+        hipLaunchKernelGGL(tau_block_kernel<16>, dim3(nq), dim3(kBlock), 0, s, a);
         break;
       }
       hipLaunchKernelGGL(select_kernel<kSelTau>, dim3(nq), dim3(kBlock), 0, s, a);
