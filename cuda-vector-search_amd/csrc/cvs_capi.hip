@@ -984,6 +984,9 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       // two query groups of one sampled chunk on one XCD: its rows come from HBM once
       pa.xcd_pair = (S.groups > 1 && S.nsample % 8 == 0) ? 1 : 0;
       pa.units = (int)S.units;
+      pa.qq_out = qq;  // the sampling scan quantises the queries on the way
+      pa.qmeta_out = qm;
+      pa.dq = (int)P.dq;
       e = launch_scan(S.cfg, kMax, pa, (int)(S.groups * S.nsample), s);
     }
     if (e != hipSuccess) return hip_fail(e, "sample pass launch");
@@ -995,7 +998,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     sa.tau = tau;
     sa.q = qh;
     sa.d = (int)d;
-    sa.qq_out = qq;
+    sa.qq_out = S.gemv ? qq : nullptr;  // (after a GEMV sampling pass the threshold select quantises)
     sa.qmeta_out = qm;
     sa.dq = (int)P.dq;
     mark(1);

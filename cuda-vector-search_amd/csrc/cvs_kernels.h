@@ -45,6 +45,9 @@ struct ScanArgs {
   int spt;            // consecutive tiles sampled by each of them
   int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles
   int units;          // units per query = nsample * (agg ? 1 : spt) * units_per_tile
+  signed char* qq_out;  // kMax: when not null, also quantise the queries for the int8 pre-filter:
+  float4* qmeta_out;    //   qq_out[nq, dq] int8 rows and qmeta_out[nq] (see cvs_q8_row.h)
+  int dq;
   // kStore*
   void* out;          // [nq, n]
   // kAppendQ8 (q, x are int8 rows viewed as 2-byte units: d = row bytes / 2)

@@ -38,6 +38,7 @@
 
 #include "cvs_common.h"
 #include "cvs_kernels.h"
+#include "cvs_q8_row.h"
 
 namespace cvs {
 
@@ -394,6 +395,21 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
   };
+
+  // kMax for the int8 pre-filter: the sampling pass also quantises the batch's
+  // queries (query i on wave i / #workgroups of workgroup i % #workgroups, so
+  // each workgroup takes at most one more query than any other), its row loads
+  // overlapping the prologue's stage loads; the threshold select that follows
+  // then only selects.
+  if constexpr (MODE == kMax) {
+    if (a.qq_out != nullptr) {
+      for (int qi = blockIdx.x + w * gridDim.x; qi < a.nq; qi += NW * gridDim.x) {
+        float v[kQ8RowPer];
+        q8_load_row(a.q + (int64_t)qi * d, d, lane, v);
+        q8_quantize_row(v, d, a.dq, a.qq_out + (int64_t)qi * a.dq, a.qmeta_out + qi, lane);
+      }
+    }
+  }
 
   // Retire the query/threshold loads (and the prologue stages) before the loop:
   // otherwise the compiler's wait-count analysis carries them around the loop
