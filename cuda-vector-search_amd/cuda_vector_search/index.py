@@ -182,7 +182,8 @@ class Index:
                 self._build_int8()
             xq, ready = self._xq, self._xq_ready
         stream = torch.cuda.current_stream(self.device)
-        stream.wait_event(ready)
+        if not ready.query():  # still being built: order this stream after the build
+            stream.wait_event(ready)
         xq.record_stream(stream)
         return xq
 
