@@ -567,7 +567,9 @@ def test_q8_build_matches_oracle(eng, n, d):
 Q8_CASES = [(1, 30000, 384, 10), (7, 20000, 320, 5), (33, 25000, 384, 64), (65, 30000, 512, 10),
             (129, 20000, 768, 100), (256, 40000, 384, 10), (300, 20000, 1024, 256), (40, 20000, 1536, 1),
             # 8-wave int8 kernels with a sampled threshold and a partial last tile
-            (256, 300001, 384, 10), (200, 262193, 768, 16)]
+            (256, 300001, 384, 10), (200, 262193, 768, 16),
+            # the 384-byte-row scan (batches above 128): a ragged last query group, d < 384
+            (129, 70001, 320, 7), (255, 65536, 384, 33)]
 
 
 @pytest.mark.gpu
@@ -615,6 +617,32 @@ def test_q8_overflowing_lists_are_rescanned(eng):
         assert plan1[0].item() == 1
         assert i1[0].cpu().tolist() == list(range(5000, 5000 + k))
         np.testing.assert_allclose(v1.cpu().numpy(), v8[:1].cpu().numpy(), rtol=0, atol=2e-6)
+
+
+@pytest.mark.gpu
+def test_q8_overflow_in_the_batch_scan(eng):
+    """The 384-byte-row int8 scan of batches above 128 (a ragged group of 200
+    queries): 3000 copies of query 0 and 40 of query 150 overflow those
+    queries' lists, the select rescans the overflowed chunks exactly, and every
+    other query is unaffected."""
+    say("q8 overflow, batch scan")
+    x, q = make(70001, 384, 200, seed=23)
+    x[10000:13000] = q[0]
+    x[50000:50040] = q[150]
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    for k in (10, 64):
+        v8, i8, plan = eng.q8_topk(qd, xd, xq, k)
+        v, i, _ = eng.fused_topk(qd, xd, k)
+        torch.cuda.synchronize()
+        assert plan[0].item() == 256
+        assert i8[0].cpu().tolist() == list(range(10000, 10000 + k))
+        assert set(i8[150, :min(k, 40)].cpu().tolist()) == set(range(50000, 50000 + min(k, 40)))
+        np.testing.assert_allclose(v8.cpu().numpy(), v.cpu().numpy(), rtol=0, atol=2e-6)
+        same = (i8 == i).cpu().numpy()
+        assert same.all() or np.abs((v8 - v).cpu().numpy())[~same].max() < 2e-6
+        oracle.check_exact(q.numpy(), x.numpy(), k, v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64))
 
 
 @pytest.mark.gpu
