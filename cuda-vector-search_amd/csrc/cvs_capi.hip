@@ -173,6 +173,7 @@ struct Plan {
   int64_t gemv_grid = 0, rows_per_wave = 0;
   // sampling pre-pass
   bool prepass = false;
+  bool tau_in_scan = false;  // one sampling maximum per workgroup, thresholds found by the scan
   int64_t nsample = 0, spt = 1, units = 0;
   int agg = 0;
   int upb = 8;  // gemv sampling units per block
@@ -184,7 +185,7 @@ struct Plan {
 // int8 pre-filter samples more densely: every candidate it keeps costs a
 // random row read, so a tighter threshold pays for itself).
 int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t chunks, int flags,
-              int cus, Plan* p, int64_t sample_div = 16) {
+              int cus, Plan* p, int64_t sample_div = 16, bool allow_tau_in_scan = true) {
   if (k < 1 || k > 256) return fail(CVS_ERR_INVALID, "fused_topk supports 1 <= k <= 256");
   if (k > n) return fail(CVS_ERR_INVALID, "k must not exceed the corpus size");
   if (bq < 0) return fail(CVS_ERR_INVALID, "bq must be 0 (auto) or one of 16, 32, 64, 128, 256");
@@ -270,6 +271,20 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
       // threshold is as tight as per-tile units give, from fewer values).
       P.agg = (P.spt > 1 && wgs * upt >= 32 * k) ? 1 : 0;
       P.units = wgs * (P.agg ? 1 : P.spt) * upt;
+      // A single query group of at most 32 queries whose sample fits 64
+      // workgroups (small corpora, small batches: all latency): up to 64
+      // sampled tiles, one each, one maximum per (query, workgroup), and the
+      // scan finds the k-th largest of them itself, which saves the threshold
+      // select's launch.  With >= 2k workgroups about 1.15k..1.4k rows of the
+      // sample pass that threshold (k when every row were its own unit).
+      const int64_t s_in = std::min<int64_t>({64, (int64_t)cus, (flags & CVS_FLAG_FORCE_PREPASS) ? P.ntiles : P.ntiles / 4});
+      P.tau_in_scan = allow_tau_in_scan && P.groups == 1 && bq <= 32 && s <= 64 && s_in >= 2 * k;
+      if (P.tau_in_scan) {
+        P.nsample = std::max<int64_t>(s, s_in);
+        P.spt = 1;
+        P.agg = 2;
+        P.units = P.nsample;
+      }
     }
   }
   if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
@@ -435,17 +450,22 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
       pa.units = (int)P.units;
       e = launch_scan(P.cfg, kMax, pa, (int)(P.groups * P.nsample), s);
       if (e != hipSuccess) return hip_fail(e, "sample pass launch");
-      SelectArgs sa{};
-      sa.lv = umax;
-      sa.nlists = 1;
-      sa.cap = (int)P.units;
-      sa.k = (int)k;
-      sa.tau = tau;
       mark(1);
-      e = launch_select(1, sa, (int)nq, s);
-      if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+      if (P.tau_in_scan) {  // the scan takes the k-th largest of each query's maxima itself
+        a.umax_in = umax;
+        a.units_in = (int)P.units;
+      } else {
+        SelectArgs sa{};
+        sa.lv = umax;
+        sa.nlists = 1;
+        sa.cap = (int)P.units;
+        sa.k = (int)k;
+        sa.tau = tau;
+        e = launch_select(1, sa, (int)nq, s);
+        if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+        a.tau = tau;
+      }
       mark(2);
-      a.tau = tau;
     } else {
       mark(1);
       mark(2);
@@ -824,7 +844,7 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
     return fail(CVS_ERR_INVALID, "the int8 pre-filter supports widths up to %lld, not %lld", (long long)kQ8MaxWidth,
                 (long long)d);
   Q8Plan P;
-  int rc = make_plan(nq, n, d, k, 0, 0, flags, cus, &P.sample, kQ8SampleDiv);
+  int rc = make_plan(nq, n, d, k, 0, 0, flags, cus, &P.sample, kQ8SampleDiv, false);
   if (rc != CVS_OK) return rc;
   P.dq = q8_row_bytes(d);
   const int ks = (int)(P.dq / 32);

@@ -38,6 +38,32 @@ __device__ __forceinline__ uint64_t make_key(float v, int id) {
 __device__ __forceinline__ float key_score(uint64_t key) { return order_float((uint32_t)(key >> 32)); }
 __device__ __forceinline__ int key_id(uint64_t key) { return (int)(~(uint32_t)key); }
 
+// ---- reductions over aligned groups of 8 lanes (DPP, no LDS round trip) ----
+// quad_perm [1,0,3,2] and [2,3,0,1] combine each quad; row_half_mirror (lane i
+// of an 8-lane half-row reads lane 7-i) then combines the two quads.  Every
+// lane of a group must be active.
+
+__device__ __forceinline__ int sum8_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t max8_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t min8_u32(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 // ---- s_waitcnt encodings (gfx9 family: vmcnt is 6 bits split 3:0 / 15:14) ----
 
 template <int N>

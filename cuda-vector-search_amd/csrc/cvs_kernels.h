@@ -33,6 +33,11 @@ struct ScanArgs {
   int xcd_pair;       // 1: map workgroups so a chunk's query groups share an XCD
   // kAppend
   const float* tau;   // [nq] initial thresholds, or null for -inf
+  // kAppend, small batches: when not null (and tau null), each query's initial
+  // threshold is the k-th largest of its units_in <= 64 sampling maxima
+  // umax_in[q * units_in ..], found by the scan itself
+  const float* umax_in;
+  int units_in;
   float* lv;          // [nq, nlists, cap] candidate scores
   int* li;            // [nq, nlists, cap] candidate row ids
   int* lcount;        // [nq, nlists]
@@ -43,7 +48,8 @@ struct ScanArgs {
   float* umax;        // [nq, units]
   int nsample;        // sampling workgroups per query group
   int spt;            // consecutive tiles sampled by each of them
-  int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles
+  int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles;
+                      // 2: one unit per workgroup (units = nsample)
   int units;          // units per query = nsample * (agg ? 1 : spt) * units_per_tile
   signed char* qq_out;  // kMax: when not null, also quantise the queries for the int8 pre-filter:
   float4* qmeta_out;    //   qq_out[nq, dq] int8 rows and qmeta_out[nq] (see cvs_q8_row.h)

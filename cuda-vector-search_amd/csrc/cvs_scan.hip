@@ -165,6 +165,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NBUF * STAGE];
   __shared__ int lcnt[RS][BQ];                        // entries in each owned list
   __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
+  __shared__ float mred[MODE == kMax ? RS : 1][BQ];    // kMax, agg 2: maxima of the row splits
   __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
   __shared__ int st_meta[APP ? NW : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
   __shared__ uint64_t sortbuf[MODE == kAppend ? NW * kMaxCap : 1];  // compaction scratch (int8 lists never compact)
@@ -306,11 +307,27 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     if (Q8) qm[qb] = a.qmeta[min(qwave0 + qb * MS + col, a.nq - 1)];
     else qm[qb] = float4{0.f, 0.f, 0.f, 0.f};
   }
+  // kAppend from sampling maxima (small batches): each query's threshold is the
+  // k-th largest of its units_in <= 64 maxima, found by 8 lanes of 8 maxima
+  // each (below, once the prologue's loads have retired).  The maxima load here
+  // beside the other prologue loads: unconditionally, from clamped addresses, so
+  // that they issue back to back.
+  constexpr bool TIN = (MODE == kAppend) && (BQ <= NT / 8);
+  const bool thr_in = TIN && a.umax_in != nullptr;
+  float kraw[TIN ? 8 : 1];
+  if constexpr (TIN) {
+    if (thr_in) {
+      const int qi = min(grp * BQ + min(tid >> 3, BQ - 1), a.nq - 1);
+      const float* src = a.umax_in + (int64_t)qi * a.units_in;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kraw[j] = src[min((tid & 7) + 8 * j, a.units_in - 1)];
+    }
+  }
   if (APP) {
     for (int i = tid; i < RS * BQ; i += NT) {
       (&lcnt[0][0])[i] = 0;
       const int qi = grp * BQ + i % BQ;
-      (&thr_s[0][0])[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+      if (!thr_in) (&thr_s[0][0])[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
     }
   }
   int st_n = 0;  // wave-uniform count of staged lane-rows
@@ -416,6 +433,50 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // back-edge and waits on vmcnt(0) at every stage.
   wait_vmcnt<0>();
 
+  // The thresholds from sampling maxima: the threshold select's bit search
+  // (count the maxima >= each candidate, summed over the 8 lanes by DPP),
+  // started below the bits that the smallest and the largest maximum share
+  // (the k-th largest lies between them) and stopped above the low
+  // kThrLowBits bits, which leaves a valid lower bound at most 2^-11 of the
+  // score below the exact k-th.  Written to LDS; every lane reads its
+  // queries' after the prologue's barrier.
+  if constexpr (TIN) {
+    if (thr_in && (tid >> 3) < BQ) {  // whole waves: BQ is a multiple of 8
+      constexpr int kThrLowBits = 12;
+      const int ql = tid >> 3, g8 = tid & 7;
+      const int qi = grp * BQ + ql;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(kraw[j]));  // keeps the uses (and their wait) here
+      uint32_t key[8], hi = 0u, lo = ~0u;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // maxima past units_in: key 0, and no part in lo
+        const uint32_t m = 0u - (uint32_t)(g8 + 8 * j < a.units_in);
+        key[j] = float_order(kraw[j]) & m;
+        hi = max(hi, key[j]);
+        lo = min(lo, key[j] | ~m);
+      }
+      hi = max8_u32(hi);
+      lo = min8_u32(lo);
+      uint32_t tk = 0u;
+      if (a.units_in >= a.k) {
+        const uint32_t diff = hi ^ lo;
+        const int top = diff ? 31 - __builtin_clz(diff) : -1;  // highest bit in which they differ
+        tk = (top < 0 ? hi : hi & ~((2u << top) - 1u)) & ~((1u << kThrLowBits) - 1u);
+        for (int bit = top; bit >= kThrLowBits; --bit) {
+          const uint32_t cand = tk | (1u << bit);
+          int c = 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) c += key[j] >= cand ? 1 : 0;
+          if (sum8_i32(c) >= a.k) tk = cand;
+        }
+      }
+      const float tv = qi >= a.nq ? __builtin_inff() : (a.units_in >= a.k ? order_float(tk) : -__builtin_inff());
+      if (g8 == 0)
+#pragma unroll
+        for (int r = 0; r < RS; ++r) thr_s[r][ql] = tv;
+    }
+  }
+
   // A fragments of one stage (KPS k-steps x RB row blocks), read from LDS one
   // stage ahead of the MFMAs that consume them.
   // A fragment of k-step kk, row block rb: row R = (rs*RB + rb)*MS + col, its
@@ -469,6 +530,10 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   };
   wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
   __builtin_amdgcn_s_barrier();           // ... and for every wave
+  if (thr_in) {  // thresholds from sampling maxima, found above
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
+  }
   if (KRING) {
 #pragma unroll
     for (int g = 0; g < LA; ++g) read_ks(0, g, fr[g]);
@@ -740,7 +805,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
   if (APP && st_n > 0) flush();
-  if (MODE == kMax && a.agg) {
+  if (MODE == kMax && a.agg == 1) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
@@ -752,6 +817,25 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // handed to another one, and make all list counts final.
   wait_vmcnt_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
+  if constexpr (MODE == kMax) {
+    if (a.agg == 2) {  // one unit per workgroup: the maxima of its lane groups and row splits
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float m = umx[qb];
+#pragma unroll
+        for (int off = MS; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (kg == 0) mred[rs][qs * QW + qb * MS + col] = m;
+      }
+      __syncthreads();
+      for (int i = tid; i < BQ; i += NT) {
+        const int qi = grp * BQ + i;
+        float m = mred[0][i];
+#pragma unroll
+        for (int r = 1; r < RS; ++r) m = fmaxf(m, mred[r][i]);
+        if (qi < a.nq) a.umax[(int64_t)qi * a.units + chunk] = m;
+      }
+    }
+  }
   if (APP) {
     for (int i = tid; i < RS * BQ; i += NT) {
       const int r = i / BQ;

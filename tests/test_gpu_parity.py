@@ -231,7 +231,12 @@ def test_gemv_path_matches_oracle_and_scan(eng, d, k):
 
 
 @pytest.mark.parametrize("flags", [0, _ext.FLAG_NO_PREPASS, _ext.FLAG_FORCE_PREPASS])
-@pytest.mark.parametrize("n,d,b,k", [(60000, 384, 256, 10), (60000, 768, 200, 100), (9000, 256, 33, 64)])
+# (100000, 384, 32, 10) and the three after it sample up to 64 tiles, one maximum
+# per (query, sampling workgroup), and the scan finds each query's threshold
+# itself (one query group of <= 32); the last samples every tile of its corpus.
+@pytest.mark.parametrize("n,d,b,k", [(60000, 384, 256, 10), (60000, 768, 200, 100), (9000, 256, 33, 64),
+                                     (100000, 384, 32, 10), (40000, 384, 13, 32), (20000, 768, 5, 16),
+                                     (3000, 128, 20, 5)])
 def test_prepass_does_not_change_results(eng, flags, n, d, b, k):
     say(f"prepass flags={flags} n={n} d={d} b={b} k={k}")
     x, q = make(n, d, b, seed=n + b)
