@@ -55,7 +55,7 @@ typedef SelSharedT<1> RowShared;  // no list offsets: ~38 KB, several workgroups
 // Cuts keys[0..nb) down to its k largest keys (nb > k), in place and in any
 // order, and returns the k-th largest key.  Whole block.
 template <class SH>
-__device__ uint64_t block_keep_top(SH& S, int nb, int k) {
+__device__ __forceinline__ uint64_t block_keep_top(SH& S, int nb, int k) {
   const int tid = threadIdx.x;
   const int w = tid / kWave;
   const int lane = tid % kWave;
@@ -122,7 +122,7 @@ __device__ uint64_t block_keep_top(SH& S, int nb, int k) {
 }
 
 // Descending bitonic sort of keys[0..N) (N a power of two), whole block.
-__device__ void block_sort_desc(uint64_t* keys, int N) {
+__device__ __forceinline__ void block_sort_desc(uint64_t* keys, int N) {
   const int tid = threadIdx.x;
   for (int size = 2; size <= N; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -146,7 +146,7 @@ __device__ void block_sort_desc(uint64_t* keys, int N) {
 // 0..nb-1) and moves its key to that slot.  Two barriers instead of the
 // bitonic network's log2(N)(log2(N)+1)/2; every lane reads the same key at a
 // time (an LDS broadcast).  Whole block.
-__device__ void block_rank_sort(uint64_t* keys, int nb) {
+__device__ __forceinline__ void block_rank_sort(uint64_t* keys, int nb) {
   const int tid = threadIdx.x;
   uint64_t mine = 0;
   int rank = 0;
@@ -160,7 +160,7 @@ __device__ void block_rank_sort(uint64_t* keys, int nb) {
 }
 
 // Descending sort of keys[0..nb) (nb <= kBuf / 2 when nb > kBlock).  Whole block.
-__device__ void block_sort_keys(uint64_t* keys, int nb) {
+__device__ __forceinline__ void block_sort_keys(uint64_t* keys, int nb) {
   if (nb <= kBlock) {
     block_rank_sort(keys, nb);
     return;
@@ -184,6 +184,27 @@ __device__ __forceinline__ int list_len(const SelectArgs& a, int q, int L, bool 
   return c;
 }
 
+// Corpus rows of the companion rows ids[0..N): out[j] = perm[ids[j]] (ids[j]
+// when perm is null), -1 for ids outside [0, n).  The lookups are
+// unconditional (index 0 stands in for the invalid ids) so that all N issue
+// back to back: behind a per-lane branch each one waits for the one before.
+template <int N>
+__device__ __forceinline__ void map_rows(const int (&ids)[N], int (&out)[N], const int* perm, int n) {
+  bool ok[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) ok[j] = ids[j] >= 0 && ids[j] < n;
+  if (perm != nullptr && n > 0) {
+    int r[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) r[j] = perm[ok[j] ? ids[j] : 0];
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = ok[j] ? r[j] : -1;
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = ok[j] ? ids[j] : -1;
+  }
+}
+
 // Exclusive prefix sums of query q's list lengths into S.pre[0..NL], and an
 // empty key buffer.  Each thread reads the counts of its (at most 32)
 // consecutive lists once.  In rescore mode a list whose count exceeds cap
@@ -191,7 +212,7 @@ __device__ __forceinline__ int list_len(const SelectArgs& a, int q, int L, bool 
 // `ovf` (zeroed by the caller) and *any_ovf becomes 1.  Whole block; returns
 // the total (S.pre[NL]).
 template <class SH>
-__device__ int list_prefix(SH& S, const SelectArgs& a, int q, bool rescore, unsigned* ovf = nullptr,
+__device__ __forceinline__ int list_prefix(SH& S, const SelectArgs& a, int q, bool rescore, unsigned* ovf = nullptr,
                            int* any_ovf = nullptr) {
   constexpr int kPer = kSelectMaxLists / kBlock;
   const int tid = threadIdx.x;
@@ -273,7 +294,7 @@ __device__ __forceinline__ int list_of(const SH& S, int NL, int gi) {
 
 // Smallest of keys[0..nb) (~0 when nb == 0).  Whole block; `red` is kWaves
 // words of LDS.
-__device__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
+__device__ __forceinline__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
   const int tid = threadIdx.x;
   uint64_t m = ~0ull;
   for (int i = tid; i < nb; i += kBlock) m = min(m, keys[i]);
@@ -295,7 +316,7 @@ __device__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
 // three or four per 8-bit digit.  Returns 0 and leaves the buffer alone when
 // m would exceed `limit` (many keys sharing a score).  Whole block; nb > k.
 template <class SH>
-__device__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
+__device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
   constexpr int PER = kBuf / kBlock;
   __shared__ float mm[2][kWaves];
   const int tid = threadIdx.x;
@@ -449,21 +470,25 @@ __device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
 }
 
 
-// Sorts the nb (<= k) surviving keys and writes row q of the outputs, padded
-// with (-inf, -1).  Whole block.
-__device__ void write_topk(SelShared& S, const SelectArgs& a, int q, int nb) {
-  const int tid = threadIdx.x;
+// Writes row q of the outputs from the descending keys[0..nb) (nb <= k),
+// padded with (-inf, -1).  Whole block.
+__device__ __forceinline__ void write_keys(const uint64_t* keys, const SelectArgs& a, int q, int nb) {
   const int k = a.k;
-  block_sort_keys(S.keys, nb);
-  for (int r = tid; r < k; r += kBlock) {
+  for (int r = threadIdx.x; r < k; r += kBlock) {
     const bool ok = r < nb;
-    a.out_v[(int64_t)q * k + r] = ok ? key_score(S.keys[r]) : -__builtin_inff();
-    const int id = ok ? key_id(S.keys[r]) : -1;
+    a.out_v[(int64_t)q * k + r] = ok ? key_score(keys[r]) : -__builtin_inff();
+    const int id = ok ? key_id(keys[r]) : -1;
     if (a.ids64)
       ((int64_t*)a.out_i)[(int64_t)q * k + r] = id;
     else
       ((int*)a.out_i)[(int64_t)q * k + r] = id;
   }
+}
+
+// Sorts the nb (<= k) surviving keys and writes row q of the outputs.  Whole block.
+__device__ __forceinline__ void write_topk(SelShared& S, const SelectArgs& a, int q, int nb) {
+  block_sort_keys(S.keys, nb);
+  write_keys(S.keys, a, q, nb);
 }
 
 // Final and threshold modes: query blockIdx.x's candidate keys are streamed
@@ -628,10 +653,24 @@ struct RescoreShape {
   static constexpr int RU = MODE == kSelRescoreWide ? 1 : MODE == kSelRescoreMid ? 2 : 4;
 };
 
+// This lane's query pieces for rescore_rows: piece l16 + 16 p of row q.
+template <int RL>
+__device__ __forceinline__ void load_query_pieces(const SelectArgs& a, int q, half8 (&qv)[RL]) {
+  const int l16 = threadIdx.x & 15;
+  const int nd = a.d / 8;
+  const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
+#pragma unroll
+  for (int p = 0; p < RL; ++p) {
+    const int c = l16 + 16 * p;
+    qv[p] = c < nd ? qr[c] : half8{};
+  }
+}
+
 // Exact fp32 scores (v_dot2_f32_f16) of the rows sids[0..m) against the query
-// fragments qv; keys above t are appended to S.keys.  Whole block.
+// fragments qv; keys above t are appended to out[0..), *cnt counting them.
+// Whole block.
 template <int RL, int RU>
-__device__ __forceinline__ void rescore_rows(SelShared& S, const int* sids, int m, uint64_t t,
+__device__ __forceinline__ void rescore_rows(uint64_t* out, int* cnt, const int* sids, int m, uint64_t t,
                                              const half8 (&qv)[RL], const _Float16* x, int d) {
   const int l16 = threadIdx.x & 15;
   const int nd = d / 8;
@@ -662,10 +701,178 @@ __device__ __forceinline__ void rescore_rows(SelShared& S, const int* sids, int 
       for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
       if (l16 == 0 && idu[u] >= 0) {
         const uint64_t key = make_key(acc, idu[u]);
-        if (key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
+        if (key > t) out[atomicAdd(cnt, 1)] = key;
       }
     }
   }
+}
+
+// The int8 final stage in one pass over the candidates, when no list
+// overflowed and there are at most 2 * kBuf of them: every entry is read once
+// into LDS as a (U, corpus row) key (S.keys, then exb); the keys of the top
+// bins of a 256-bin histogram of U (m >= k of them, at most kBlock) are
+// rescored, and the k-th best of their exact keys, kappa, bounds the final
+// k-th best key from below (they are real rows); then every other candidate
+// whose U reaches score(kappa) is rescored at once (a candidate below it has
+// S' <= U < score(kappa) and cannot enter).  The same rows' exact keys as the
+// general path below, so the same top k.  Returns false, having written
+// nothing, when the top bins hold more than kBlock keys or the second round
+// more than kBuf - k rows (many equal bounds); the general path then runs.
+// Whole block.
+template <int RL, int RU>
+__device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64_t* ex1, int* sids,
+                                             const SelectArgs& a, int q, int total) {
+  constexpr int PER = 2 * kBuf / kBlock;
+  constexpr int G8 = 8;
+  __shared__ float mm[2][kWaves];
+  __shared__ int cnt[2];  // exact keys; rows in sids
+  __shared__ uint64_t red[kWaves];
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  const int lane = tid % kWave;
+  const int NL = a.nlists;
+  const int k = a.k;
+  auto cand = [&](int i) -> uint64_t& { return i < kBuf ? S.keys[i] : exb[i - kBuf]; };
+  for (int i = tid; i < kWaves * 256; i += kBlock) (&S.hist[0][0])[i] = 0;
+  if (tid == 0) {
+    cnt[0] = 0;
+    cnt[1] = 0;
+  }
+  // every entry, 8 per thread at a time: list lookups, then the loads, then
+  // the row map (each a batch of independent accesses); key 0 marks an
+  // invalid row id
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+  for (int j0 = 0; j0 < PER && j0 * kBlock < total; j0 += G8) {
+    int lst[G8];
+#pragma unroll
+    for (int j = 0; j < G8; ++j) {
+      const int gi = (j0 + j) * kBlock + tid;
+      lst[j] = gi < total ? list_of(S, NL, gi) : -1;
+    }
+    int idv[G8];
+    float uv[G8];
+#pragma unroll
+    for (int j = 0; j < G8; ++j) {
+      idv[j] = -1;
+      uv[j] = 0.f;
+      if (lst[j] >= 0) {
+        const int64_t off = ((int64_t)q * NL + lst[j]) * a.cap + ((j0 + j) * kBlock + tid - S.pre[lst[j]]);
+        idv[j] = a.li[off];
+        uv[j] = a.lv[off];
+      }
+    }
+    map_rows(idv, idv, a.perm, (int)a.n);
+#pragma unroll
+    for (int j = 0; j < G8; ++j) {
+      if (idv[j] >= 0) {
+        lo = fminf(lo, uv[j]);
+        hi = fmaxf(hi, uv[j]);
+      }
+      if (lst[j] >= 0) cand((j0 + j) * kBlock + tid) = idv[j] >= 0 ? make_key(uv[j], idv[j]) : 0ull;
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off));
+    hi = fmaxf(hi, __shfl_xor(hi, off));
+  }
+  if (lane == 0) {
+    mm[0][w] = lo;
+    mm[1][w] = hi;
+  }
+  __syncthreads();
+  lo = mm[0][0];
+  hi = mm[1][0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    lo = fminf(lo, mm[0][i]);
+    hi = fmaxf(hi, mm[1][i]);
+  }
+  // bin(U) as in block_cut_hist: non-decreasing, in [0, 255] whatever the bounds
+  const bool span = hi > lo && __builtin_isfinite(lo) && __builtin_isfinite(hi);
+  const float scale = span ? 256.0f / (hi - lo) : 0.0f;
+  auto bin = [&](uint64_t kk) {
+    const float t = (key_score(kk) - lo) * scale;
+    return (int)(t >= 0.0f ? fminf(t, 255.0f) : 0.0f);
+  };
+  for (int i = tid; i < total; i += kBlock) {
+    const uint64_t kk = cand(i);
+    if (kk != 0ull) atomicAdd(&S.hist[w][bin(kk)], 1);
+  }
+  __syncthreads();
+  if (w == 0) {  // the highest bin b with #(keys in bins >= b) >= k; bin 0 (all) when fewer
+    int c[4];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
+      const int b = 255 - (4 * lane + j);
+      c[j] = S.hist[0][b] + S.hist[1][b] + S.hist[2][b] + S.hist[3][b];
+      sum += c[j];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int o = __shfl_up(incl, off);
+      if (lane >= off) incl += o;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (run < k && k <= run + c[j]) {
+        S.digit = 255 - (4 * lane + j);
+        S.above = run + c[j];
+      }
+      run += c[j];
+    }
+    if (lane == kWave - 1 && incl < k) {
+      S.digit = 0;
+      S.above = incl;
+    }
+  }
+  __syncthreads();
+  const int bstar = S.digit;
+  if (S.above > kBlock) return false;
+  // round 1: the top bins' rows
+  for (int i = tid; i < total; i += kBlock) {
+    const uint64_t kk = cand(i);
+    if (kk != 0ull && bin(kk) >= bstar) sids[atomicAdd(&cnt[1], 1)] = key_id(kk);
+  }
+  __syncthreads();
+  const int m1 = cnt[1];
+  half8 qv[RL];
+  load_query_pieces<RL>(a, q, qv);
+  rescore_rows<RL, RU>(ex1, &cnt[0], sids, m1, 0ull, qv, a.x, a.d);
+  __syncthreads();
+  uint64_t kap = 0ull;  // k-th best exact key of round 1 (0: fewer than k rows in all)
+  if (m1 > k) {
+    block_rank_sort(ex1, m1);  // m1 <= kBlock; the k best first
+    kap = ex1[k - 1];
+  } else if (m1 == k) {
+    kap = block_min_key(ex1, k, red);
+  }
+  const int k1 = min(m1, k);
+  if (tid == 0) cnt[1] = 0;
+  __syncthreads();
+  // round 2: every other row whose bound reaches score(kappa)
+  if (kap != 0ull) {
+    const float umin = key_score(kap);
+    for (int i = tid; i < total; i += kBlock) {
+      const uint64_t kk = cand(i);
+      if (kk != 0ull && bin(kk) < bstar && key_score(kk) >= umin) sids[atomicAdd(&cnt[1], 1)] = key_id(kk);
+    }
+  }
+  __syncthreads();
+  const int m2 = cnt[1];
+  if (k1 + m2 > kBuf) return false;
+  for (int i = tid; i < k1; i += kBlock) exb[i] = ex1[i];  // (the candidates are no longer needed)
+  if (tid == 0) cnt[0] = k1;
+  __syncthreads();
+  rescore_rows<RL, RU>(exb, &cnt[0], sids, m2, kap, qv, a.x, a.d);
+  __syncthreads();
+  const int nex = cnt[0];
+  block_sort_keys(exb, nex);
+  write_keys(exb, a, q, min(nex, k));
+  return true;
 }
 
 // Final stage of the int8 pre-filter: the exact top-k of query blockIdx.x from
@@ -692,7 +899,9 @@ template <int MODE>
 __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
   __shared__ SelShared S;
   constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
-  __shared__ int sids[kBatch];                    // rows to rescore
+  __shared__ int sids[2 * kBuf];                  // rows to rescore
+  __shared__ uint64_t ex[kBuf];                   // one-pass form: candidates past kBuf, then exact keys
+  __shared__ uint64_t ex1[kBlock];                // one-pass form: round 1's exact keys
   __shared__ unsigned ovf[kSelectMaxLists / 32];  // overflowed-list bitmap
   __shared__ uint64_t red[kWaves];
   __shared__ int nrows;
@@ -701,21 +910,13 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
   const int q = blockIdx.x;
   const int NL = a.nlists;
   const int k = a.k;
-  const int l16 = tid & 15;
-  half8 qv[RL];
-  {
-    const int nd = a.d / 8;
-    const half8* qr = reinterpret_cast<const half8*>(a.q + (int64_t)q * a.d);
-#pragma unroll
-    for (int p = 0; p < RL; ++p) {
-      const int c = l16 + 16 * p;
-      qv[p] = c < nd ? qr[c] : half8{};
-    }
-  }
   for (int i = tid; i < (NL + 31) / 32; i += kBlock) ovf[i] = 0u;
   if (tid == 0) any_ovf = 0;
   __syncthreads();
   const int total = list_prefix(S, a, q, true, ovf, &any_ovf);
+  if (!a.exact && !any_ovf && total <= 2 * kBuf && final_in_lds<RL, RU>(S, ex, ex1, sids, a, q, total)) return;
+  half8 qv[RL];
+  load_query_pieces<RL>(a, q, qv);
   auto overflowed = [&](int L) { return ((ovf[L >> 5] >> (L & 31)) & 1u) != 0; };
 
   // Phase 1: the k largest (U, id) keys of the lists that did not overflow.
@@ -737,11 +938,7 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < kGather; ++j) {  // companion rows -> corpus rows
-      if (idv[j] < 0 || idv[j] >= a.n) idv[j] = -1;
-      else if (a.perm) idv[j] = a.perm[idv[j]];
-    }
+    map_rows(idv, idv, a.perm, (int)a.n);  // companion rows -> corpus rows
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const uint64_t key = make_key(val[j], idv[j]);
@@ -782,7 +979,7 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
       S.thr_key = 0ull;
     }
     __syncthreads();
-    rescore_rows<RL, RU>(S, sids, n1, 0ull, qv, a.x, a.d);
+    rescore_rows<RL, RU>(S.keys, &S.nbuf, sids, n1, 0ull, qv, a.x, a.d);
     __syncthreads();
     if (n1 > k) {  // n1 <= kBlock: sort, keep the k best
       block_rank_sort(S.keys, S.nbuf);
@@ -830,16 +1027,15 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
         }
       }
     }
+    map_rows(idv, idv, a.perm, (int)a.n);  // companion rows -> corpus rows
 #pragma unroll
-    for (int j = 0; j < kGather; ++j) {  // companion rows -> corpus rows; list entries phase 1 kept are out
-      if (idv[j] >= 0 && a.perm) idv[j] = a.perm[idv[j]];
+    for (int j = 0; j < kGather; ++j)  // list entries phase 1 kept are out
       if (fromlist[j] && make_key(uv[j], idv[j]) >= ucut) idv[j] = -1;
-    }
 #pragma unroll
     for (int j = 0; j < kGather; ++j)
       if (idv[j] >= 0) sids[atomicAdd(&nrows, 1)] = idv[j];
     __syncthreads();
-    rescore_rows<RL, RU>(S, sids, nrows, t, qv, a.x, a.d);
+    rescore_rows<RL, RU>(S.keys, &S.nbuf, sids, nrows, t, qv, a.x, a.d);
     end_batch(S, k, base + kBatch >= total);
   }
   write_topk(S, a, q, min(S.nbuf, k));
@@ -927,10 +1123,9 @@ __global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
     }
     int xrv[kGather];
 #pragma unroll
-    for (int j = 0; j < kGather; ++j) {
+    for (int j = 0; j < kGather; ++j)
       if (idv[j] < 0 || idv[j] >= a.n) idv[j] = -1;
-      xrv[j] = (idv[j] >= 0 && a.perm) ? a.perm[idv[j]] : idv[j];
-    }
+    map_rows(idv, xrv, a.perm, (int)a.n);
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const int i = j * kBlock + tid;
