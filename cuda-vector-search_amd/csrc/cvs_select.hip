@@ -152,7 +152,8 @@ __device__ __forceinline__ void block_rank_sort(uint64_t* keys, int nb) {
   int rank = 0;
   if (tid < nb) {
     mine = keys[tid];
-    for (int i = 0; i < nb; ++i) rank += keys[i] > mine ? 1 : 0;
+#pragma unroll 8
+    for (int i = 0; i < nb; ++i) rank += keys[i] > mine ? 1 : 0;  // (reads in flight together)
   }
   __syncthreads();
   if (tid < nb) keys[rank] = mine;
@@ -203,6 +204,27 @@ __device__ __forceinline__ void map_rows(const int (&ids)[N], int (&out)[N], con
 #pragma unroll
     for (int j = 0; j < N; ++j) out[j] = ok[j] ? ids[j] : -1;
   }
+}
+
+// sids[0..m) <- perm[sids[0..m)] (nothing when perm is null), 8 independent
+// lookups per thread at a time.  Whole block; ends with a barrier.
+__device__ __forceinline__ void map_sids(int* sids, int m, const int* perm) {
+  if (perm != nullptr) {
+    for (int b0 = 0; b0 < m; b0 += 8 * kBlock) {
+      int r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = b0 + j * kBlock + threadIdx.x;
+        r[j] = perm[i < m ? sids[i] : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = b0 + j * kBlock + threadIdx.x;
+        if (i < m) sids[i] = r[j];
+      }
+    }
+  }
+  __syncthreads();
 }
 
 // Exclusive prefix sums of query q's list lengths into S.pre[0..NL], and an
@@ -738,16 +760,24 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
     cnt[0] = 0;
     cnt[1] = 0;
   }
-  // every entry, 8 per thread at a time: list lookups, then the loads, then
-  // the row map (each a batch of independent accesses); key 0 marks an
-  // invalid row id
+  // every entry, 8 per thread at a time (list lookups, then the loads, then
+  // the row map when few), as a (U, row) key; key 0 marks an invalid row id.
+  // Of thousands of candidates only the rows rescored (hundreds) are mapped to
+  // corpus rows, by map_sids (a random 4-byte lookup costs a whole cache
+  // line); of a few hundred, all are, on the way (saving map_sids' round trips).
+  const bool map_now = total <= 1024;
+  // the list of every entry, written by the list's thread into sids (free
+  // until round 1): one LDS read per entry instead of a binary search
+  for (int L = tid; L < NL; L += kBlock)
+    for (int i = S.pre[L], e = S.pre[L + 1]; i < e; ++i) sids[i] = L;
+  __syncthreads();
   float lo = __builtin_inff(), hi = -__builtin_inff();
   for (int j0 = 0; j0 < PER && j0 * kBlock < total; j0 += G8) {
     int lst[G8];
 #pragma unroll
     for (int j = 0; j < G8; ++j) {
       const int gi = (j0 + j) * kBlock + tid;
-      lst[j] = gi < total ? list_of(S, NL, gi) : -1;
+      lst[j] = gi < total ? sids[gi] : -1;
     }
     int idv[G8];
     float uv[G8];
@@ -761,14 +791,15 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
         uv[j] = a.lv[off];
       }
     }
-    map_rows(idv, idv, a.perm, (int)a.n);
+    if (map_now) map_rows(idv, idv, a.perm, (int)a.n);
 #pragma unroll
     for (int j = 0; j < G8; ++j) {
-      if (idv[j] >= 0) {
+      const bool ok = idv[j] >= 0 && idv[j] < a.n;
+      if (ok) {
         lo = fminf(lo, uv[j]);
         hi = fmaxf(hi, uv[j]);
       }
-      if (lst[j] >= 0) cand((j0 + j) * kBlock + tid) = idv[j] >= 0 ? make_key(uv[j], idv[j]) : 0ull;
+      if (lst[j] >= 0) cand((j0 + j) * kBlock + tid) = ok ? make_key(uv[j], idv[j]) : 0ull;
     }
   }
 #pragma unroll
@@ -839,6 +870,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   }
   __syncthreads();
   const int m1 = cnt[1];
+  map_sids(sids, m1, map_now ? nullptr : a.perm);
   half8 qv[RL];
   load_query_pieces<RL>(a, q, qv);
   rescore_rows<RL, RU>(ex1, &cnt[0], sids, m1, 0ull, qv, a.x, a.d);
@@ -866,7 +898,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   if (k1 + m2 > kBuf) return false;
   for (int i = tid; i < k1; i += kBlock) exb[i] = ex1[i];  // (the candidates are no longer needed)
   if (tid == 0) cnt[0] = k1;
-  __syncthreads();
+  map_sids(sids, m2, map_now ? nullptr : a.perm);
   rescore_rows<RL, RU>(exb, &cnt[0], sids, m2, kap, qv, a.x, a.d);
   __syncthreads();
   const int nex = cnt[0];
