@@ -836,7 +836,13 @@ struct Q8Plan {
   ScanCfg cfg{};
   int64_t dq = 0, bq = 0, groups = 1, chunks = 1, ntiles = 0, tpc = 0, nlists = 0, cap = 0;
   int xcd_pair = 0;
-  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_qq = 0, off_qm = 0, ws_bytes = 0;
+  // int8 sampling pass (scan mode kMaxQ8) over about 1/kQ8SampleDiv of the
+  // int8 tiles, instead of the fp16 one (`sample`) for batches
+  bool s8 = false;
+  int64_t s8_nsample = 0, s8_spt = 1, s8_units = 0;
+  int s8_agg = 0;
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_uarg = 0, off_qq = 0, off_qm = 0,
+          ws_bytes = 0;
 };
 
 int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus, Q8Plan* out) {
@@ -890,6 +896,26 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
     P.chunks = c;
     P.xcd_pair = (P.groups > 1 && c % 8 == 0) ? 1 : 0;
     P.nlists = c * rs;
+    // The int8 sampling pass: the fp16 pass's tile count and unit layout on
+    // the int8 tiles (half the bytes, the int8 MFMA), with each unit's row
+    // kept so that the threshold select can rescore the rows of the largest
+    // maxima exactly.  A workgroup sampling several tiles keeps one unit per
+    // (row split, lane group) over all of them and writes it once at the end
+    // (per-tile units for k = 100 at 1M x 768 cost 7 us more in the scattered
+    // stores and in the threshold select than the looser threshold costs
+    // later).  At most 16 * 256 units per query (the threshold kernel's limit).
+    const int64_t upt = P.cfg.units_per_tile();
+    int64_t s = std::min<int64_t>(16384 / kQ8SampleDiv, std::max<int64_t>(P.ntiles / kQ8SampleDiv, ceil_div(8 * k, upt)));
+    s = std::min<int64_t>(s, (flags & CVS_FLAG_FORCE_PREPASS) ? P.ntiles : P.ntiles / 4);
+    P.s8 = !(flags & CVS_FLAG_NO_PREPASS) &&
+           (((flags & CVS_FLAG_FORCE_PREPASS) && s >= 1) || (s >= 4 && s * upt >= 2 * k));
+    if (P.s8) {
+      const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>({s, cus / P.groups, (16 * 256) / upt}));
+      P.s8_spt = std::max<int64_t>(1, s / wgs);
+      P.s8_nsample = wgs;
+      P.s8_agg = P.s8_spt > 1 ? 1 : 0;
+      P.s8_units = wgs * (P.s8_agg ? 1 : P.s8_spt) * upt;
+    }
   }
   P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
   if (P.groups * P.chunks > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
@@ -905,7 +931,13 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   P.off_tau = off;
   off = align_up(off + nqq * 4, 256);
   P.off_umax = off;
-  if (P.sample.prepass) off = align_up(off + nqq * P.sample.units * 4, 256);
+  if (P.s8) {
+    off = align_up(off + nqq * P.s8_units * 4, 256);
+    P.off_uarg = off;
+    off = align_up(off + nqq * P.s8_units * 4, 256);
+  } else if (P.sample.prepass) {
+    off = align_up(off + nqq * P.sample.units * 4, 256);
+  }
   P.off_qq = off;
   off = align_up(off + nqq * P.dq, 256);
   P.off_qm = off;
@@ -961,14 +993,59 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   const _Float16* qh = static_cast<const _Float16*>(q);
   const _Float16* xh = static_cast<const _Float16*>(x);
   const Plan& S = P.sample;
+  const bool fp16_sample = !P.s8 && S.prepass;
+  const float4* bmeta = reinterpret_cast<const float4*>(static_cast<const char*>(xq) + L.off_meta);
+  const int* perm = reinterpret_cast<const int*>(static_cast<const char*>(xq) + L.off_perm);
+  const float gamma = (float)(3 * d + 8) / 16777216.0f;
   hipError_t e;
 
-  if (!S.prepass) {  // otherwise the threshold select quantises the queries on the way
+  if (!fp16_sample) {  // otherwise the threshold select quantises the queries on the way
     Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm};
     e = launch_q8_queries(qa, s);
     if (e != hipSuccess) return hip_fail(e, "query quantisation launch");
   }
-  if (S.prepass) {  // exact fp16 sampling pre-pass and threshold, as in cvs_fused_topk
+  if (P.s8) {  // int8 sampling pass; the threshold from rescoring its best units' rows
+    ScanArgs pa{};
+    pa.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
+    pa.x = static_cast<const _Float16*>(xq);
+    pa.n = n;
+    pa.nq = (int)nq;
+    pa.d = (int)(P.dq / 2);
+    pa.groups = (int)P.groups;
+    pa.nchunks = (int)P.chunks;
+    pa.ntiles = P.ntiles;
+    pa.tpc = P.tpc;
+    pa.k = (int)k;
+    pa.cap = (int)P.cap;
+    pa.umax = umax;
+    pa.uarg = reinterpret_cast<int*>(ws + P.off_uarg);
+    pa.nsample = (int)P.s8_nsample;
+    pa.spt = (int)P.s8_spt;
+    pa.agg = P.s8_agg;
+    pa.xcd_pair = (P.groups > 1 && P.s8_nsample % 8 == 0) ? 1 : 0;
+    pa.units = (int)P.s8_units;
+    pa.qmeta = qm;
+    pa.bmeta = bmeta;
+    pa.gamma = gamma;
+    e = launch_scan(P.cfg, kMaxQ8, pa, (int)(P.groups * P.s8_nsample), s);
+    if (e != hipSuccess) return hip_fail(e, "int8 sample pass launch");
+    SelectArgs ta{};
+    ta.lv = umax;
+    ta.li = pa.uarg;
+    ta.nlists = 1;
+    ta.cap = (int)P.s8_units;
+    ta.k = (int)k;
+    ta.tau = tau;
+    ta.q = qh;
+    ta.x = xh;
+    ta.n = n;
+    ta.d = (int)d;
+    ta.perm = perm;
+    mark(1);
+    e = launch_select(5, ta, (int)nq, s);
+    if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+    mark(2);
+  } else if (fp16_sample) {  // exact fp16 sampling pre-pass and threshold, as in cvs_fused_topk
     if (S.gemv) {
       GemvArgs pg{};
       pg.q = qh;
@@ -1029,8 +1106,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     mark(1);
     mark(2);
   }
-  const float4* bmeta = reinterpret_cast<const float4*>(static_cast<const char*>(xq) + L.off_meta);
-  const float gamma = (float)(3 * d + 8) / 16777216.0f;
+  const bool have_tau = P.s8 || S.prepass;
   if (P.gemv) {
     GemvArgs g{};
     g.q = reinterpret_cast<const _Float16*>(qq);
@@ -1038,7 +1114,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     g.n = n;
     g.d = (int)P.dq;  // int8 row bytes
     g.rows_per_wave = P.rows_per_wave;
-    g.tau = S.prepass ? tau : nullptr;
+    g.tau = have_tau ? tau : nullptr;
     g.lv = lv;
     g.li = li;
     g.lcount = cnt;
@@ -1063,7 +1139,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     a.ntiles = P.ntiles;
     a.tpc = P.tpc;
     a.xcd_pair = P.xcd_pair;
-    a.tau = S.prepass ? tau : nullptr;
+    a.tau = have_tau ? tau : nullptr;
     a.lv = lv;
     a.li = li;
     a.lcount = cnt;
@@ -1097,7 +1173,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   fa.d = (int)d;
   fa.ntiles = P.ntiles;
   fa.tpc = P.tpc;
-  fa.perm = reinterpret_cast<const int*>(static_cast<const char*>(xq) + L.off_perm);
+  fa.perm = perm;
   if (P.gemv) {  // list L = rows [L * rows_per_wave, (L + 1) * rows_per_wave)
     fa.tile_rows = (int)P.rows_per_wave;
     fa.wave_rows = (int)P.rows_per_wave;
@@ -1111,7 +1187,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     // rescoring spread over about 4 workgroups per CU, (query, group of lists)
     // each; the select then sees exact scores
     fa.exact = 1;
-    fa.tau_in = S.prepass ? tau : nullptr;
+    fa.tau_in = have_tau ? tau : nullptr;
     fa.qmeta = qm;
     fa.xmax = reinterpret_cast<const float*>(static_cast<const char*>(xq) + L.off_xmax);
     fa.gamma = (float)d / 16777216.0f;

@@ -14,6 +14,8 @@ enum ScanMode : int {
   kStoreF16 = 3,  // write the full score matrix (fp16)
   kAppendQ8 = 4,  // int8 pre-filter: int8 rows x int8 queries, append rows whose score
                   // upper bound reaches the threshold (no compaction; full lists overflow)
+  kMaxQ8 = 5,     // int8 sample pass: per-(query, unit) largest approximate score
+                  // A = s_q s_b sum(q~ x~) over disjoint row sets, and its row
 };
 
 // One tile of corpus rows is scored against a group of queries by one
@@ -46,6 +48,7 @@ struct ScanArgs {
   int k;
   // kMax
   float* umax;        // [nq, units]
+  int* uarg;          // kMaxQ8: [nq, units] the (companion) row of each unit's maximum
   int nsample;        // sampling workgroups per query group
   int spt;            // consecutive tiles sampled by each of them
   int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles;
@@ -199,7 +202,9 @@ hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid
 bool q8scan384_fits(const ScanArgs& a);
 hipError_t launch_q8scan384(const ScanArgs& a, int grid, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs& a, int grid, hipStream_t s);  // any d % 64 == 0 (int8: 384/768/1536 bytes)
-hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);  // 0 final, 1 threshold, 2 rescore
+// mode 0 final, 1 threshold, 2 rescore, 5 threshold from an int8 sampling pass
+// (lv / li: each unit's approximate maximum and its companion row, cap units)
+hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_rescore(const SelectArgs& a, int nq, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
 hipError_t launch_rowtopk(const RowTopkArgs& a, int blocks, hipStream_t s);

@@ -97,6 +97,10 @@ template <>
 struct MfmaFor<32, kAppendQ8> {
   typedef MfmaI8 type;
 };
+template <>
+struct MfmaFor<32, kMaxQ8> {
+  typedef MfmaI8 type;
+};
 
 // FULLW: the row width is exactly KSMAX * KSZ, so the stage count is a
 // compile-time constant (per-stage guards on a runtime count split the
@@ -109,8 +113,9 @@ struct MfmaFor<32, kAppendQ8> {
 
 template <int MS, int QS, int QB, int RB, int KSMAX, int MODE, bool FULLW>
 __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArgs a) {
-  static_assert(MODE != kAppendQ8 || MS == 32, "int8 pre-filter uses the 32x32 MFMA");
-  static_assert(MODE != kAppendQ8 || (MS * RB <= 64 && 64 % (MS * RB) == 0),
+  constexpr bool Q8 = (MODE == kAppendQ8 || MODE == kMaxQ8);  // int8 rows and queries
+  static_assert(!Q8 || MS == 32, "int8 pre-filter uses the 32x32 MFMA");
+  static_assert(!Q8 || (MS * RB <= 64 && 64 % (MS * RB) == 0),
                 "int8 pre-filter: a wave's rows of a tile must lie in one 64-row block (one meta entry)");
   typedef typename MfmaFor<MS, MODE>::type M;
   typedef typename M::acc_t acc_t;
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // memory (measured: HBM -> LDS at 6.5 TB/s against 5.4 TB/s for stages of one
   // 128-byte line per row, whose loads read 8 lines a row apart).  Otherwise a
   // stage is one line (64 columns) of every row of the tile.
-  constexpr bool TS = FULLW && MODE == kAppendQ8 && NW == 8 && TR * KSMAX * M::KSZ * 2 == 24 * 1024;
+  constexpr bool TS = FULLW && Q8 && NW == 8 && TR * KSMAX * M::KSZ * 2 == 24 * 1024;
   constexpr int LPR = TS ? KSMAX / KSL : 1;  // lines per row in a stage
   constexpr int KPS = LPR * KSL;     // MFMA k-steps per stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int QA = QL ? ((BQ + 8 * NW - 1) / (8 * NW)) * (8 * NW) : 0;
   constexpr int FPS = FC + QA / 8;   // 1 KB DMA loads per stage
   static_assert(FPS % NW == 0, "every wave must issue the same number of stage loads");
-  static_assert(!QL || (!FULLW && MODE != kAppendQ8), "queries in LDS: fp16 rows of a runtime width");
+  static_assert(!QL || (!FULLW && !Q8), "queries in LDS: fp16 rows of a runtime width");
   constexpr int LPW = FPS / NW;      // stage loads per wave
   constexpr int STAGE = FPS * 1024;
   constexpr int NBUF = ((QS >= 4 ? 56 : 40) * 1024) / STAGE + 2;
@@ -152,8 +157,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr bool PAIR = FULLW && (NCMAX % 2 == 0) && NBUF >= 5;
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
-  constexpr bool Q8 = (MODE == kAppendQ8);
-  constexpr bool APP = (MODE == kAppend || Q8);
+  constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8);
+  constexpr bool SMAX = (MODE == kMax || MODE == kMaxQ8);  // sample passes
   constexpr int STCAP = 64;          // staged entries per wave
   // A staged entry is one lane's NE scores of one (query block, row block): a
   // row of EST floats (NE plus padding to an odd number of 16-byte units, so
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
   int64_t t_begin, t_end;
-  if (MODE == kMax) {  // spt consecutive tiles centred on an evenly spread position
+  if (SMAX) {  // spt consecutive tiles centred on an evenly spread position
     const int64_t centre = ((2 * (int64_t)chunk + 1) * a.ntiles) / (2 * (int64_t)a.nsample);
     t_begin = centre - a.spt / 2;
     if (t_begin > a.ntiles - a.spt) t_begin = a.ntiles - a.spt;
@@ -331,9 +336,13 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
   int st_n = 0;  // wave-uniform count of staged lane-rows
-  float umx[QB];  // kMax with agg: this lane's unit maxima over all sampled tiles
+  float umx[QB];  // kMax / kMaxQ8 with agg: this lane's unit maxima over all sampled tiles
+  int uag[QB];    // kMaxQ8 with agg: their rows
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) umx[qb] = -__builtin_inff();
+  for (int qb = 0; qb < QB; ++qb) {
+    umx[qb] = -__builtin_inff();
+    uag[qb] = 0;
+  }
 
   // Appends the passing scores of this wave's staged entries to its global
   // candidate lists.  A list that fills up is compacted to its k best entries
@@ -696,7 +705,39 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
-      if constexpr (Q8) {
+      if constexpr (MODE == kMaxQ8) {
+        // the largest approximate score A = cq * acc of this lane's rows (cq >=
+        // 0: that of the largest int32 sum) and its row (the first on ties)
+        if (partial) {  // rows past n of the corpus's last tile: never the maximum
+          const int64_t left = n - rowb;
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int e = 0; e < M::NE; ++e)
+              if (rb * MS + M::row(e) >= left) acc[qb][rb][e] = INT_MIN;
+        }
+        int mi = acc[qb][0][0], mr = M::row(0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int e = 0; e < M::NE; ++e)
+            if (acc[qb][rb][e] > mi) {
+              mi = acc[qb][rb][e];
+              mr = rb * MS + M::row(e);
+            }
+        const float av = mi == INT_MIN ? -__builtin_inff() : (float)mi * (qm[qb].x * bm.x);
+        const int row = (int)rowb + mr;
+        if (a.agg) {
+          if (av > umx[qb]) {
+            umx[qb] = av;
+            uag[qb] = row;
+          }
+        } else if (qi < a.nq) {
+          const int64_t u = (int64_t)qi * a.units + ((chunk * a.spt + (t - t_begin)) * RS + rs) * G + kg;
+          a.umax[u] = av;
+          a.uarg[u] = row;
+        }
+      } else if constexpr (Q8) {
         // Upper bound of each exact score: A + slack with A = cq * acc and
         // cq >= 0, so the largest bound of a row block is that of its largest
         // int32 sum (conversion and fma round monotonically): the filter needs
@@ -805,11 +846,15 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
   if (APP && st_n > 0) flush();
-  if (MODE == kMax && a.agg == 1) {
+  if (SMAX && a.agg == 1) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
-      if (qi < a.nq) a.umax[(int64_t)qi * a.units + (chunk * RS + rs) * G + kg] = umx[qb];
+      if (qi < a.nq) {
+        const int64_t u = (int64_t)qi * a.units + (chunk * RS + rs) * G + kg;
+        a.umax[u] = umx[qb];
+        if (MODE == kMaxQ8) a.uarg[u] = uag[qb];
+      }
     }
   }
 
@@ -848,9 +893,16 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 
 // int8 pre-filter: full-width rows only (the int8 row bytes are padded to 32 * KS).
 template <int MS, int QS, int QB, int RB, int KS>
-hipError_t launch_one_q8(const ScanArgs& a, int grid, hipStream_t s) {
+hipError_t launch_one_q8(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   if (a.d != KS * MfmaI8::KSZ || a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendQ8, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+  if (mode == kMaxQ8) {
+    if (a.umax == nullptr || a.uarg == nullptr || a.nsample < 1 || a.spt < 1 || a.agg < 0 || a.agg > 1)
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kMaxQ8, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendQ8, true>), dim3(grid), dim3(scan_waves(QS) * kWave), 0, s,
+                       a);
+  }
   return hipGetLastError();
 }
 
@@ -929,7 +981,7 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
 }  // namespace
 
 bool scan_cfg_available(const ScanCfg& c, int mode) {
-  if (mode == kAppendQ8) {
+  if (mode == kAppendQ8 || mode == kMaxQ8) {
 #define CVS_HAS_Q8(MS, QS, QB, RB, KS) \
   if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return true;
     CVS_SCAN_Q8_CONFIGS(CVS_HAS_Q8)
@@ -945,10 +997,10 @@ bool scan_cfg_available(const ScanCfg& c, int mode) {
 }
 
 hipError_t launch_scan(const ScanCfg& c, int mode, const ScanArgs& a, int grid, hipStream_t s) {
-  if (mode == kAppendQ8) {
+  if (mode == kAppendQ8 || mode == kMaxQ8) {
 #define CVS_LAUNCH_Q8(MS, QS, QB, RB, KS)                                      \
   if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) \
-    return launch_one_q8<MS, QS, QB, RB, KS>(a, grid, s);
+    return launch_one_q8<MS, QS, QB, RB, KS>(mode, a, grid, s);
     CVS_SCAN_Q8_CONFIGS(CVS_LAUNCH_Q8)
 #undef CVS_LAUNCH_Q8
     return hipErrorInvalidValue;

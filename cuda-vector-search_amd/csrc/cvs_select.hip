@@ -174,6 +174,7 @@ __device__ __forceinline__ void block_sort_keys(uint64_t* keys, int nb) {
 }
 
 constexpr int kSelFinal = 0, kSelTau = 1, kSelRescore = 2, kSelRescoreWide = 3, kSelRescoreMid = 4;
+constexpr int kSelTauRescore = 5;  // launch mode: threshold from an int8 sampling pass
 constexpr int kMaxD = 1536;
 
 // Entries of list L of query q: its count, or in rescore mode the size of its
@@ -331,6 +332,41 @@ __device__ __forceinline__ uint64_t block_min_key(const uint64_t* keys, int nb, 
   return r;
 }
 
+// Wave 0 of a block, over per-wave 256-bin histograms: the highest bin b such
+// that the bins >= b hold >= k counts in all, into *bstar, and that count into
+// *above (bin 0 and the whole count when it is below k).  The caller barriers
+// before (histograms complete) and after (results visible).
+__device__ __forceinline__ void hist_cut_bin(const int (*hist)[256], int k, int* bstar, int* above) {
+  const int lane = threadIdx.x % kWave;
+  int c[4];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
+    const int b = 255 - (4 * lane + j);
+    c[j] = hist[0][b] + hist[1][b] + hist[2][b] + hist[3][b];
+    sum += c[j];
+  }
+  int incl = sum;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  int run = incl - sum;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (run < k && k <= run + c[j]) {
+      *bstar = 255 - (4 * lane + j);
+      *above = run + c[j];
+    }
+    run += c[j];
+  }
+  if (lane == kWave - 1 && incl < k) {
+    *bstar = 0;
+    *above = incl;
+  }
+}
+
 // Loose cut of the buffer's keys by score: a 256-bin histogram over the
 // scores' [min, max] picks the fewest top bins holding at least k keys, and
 // every key in them (m >= k keys, exactly those >= the returned key) is kept,
@@ -388,29 +424,7 @@ __device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int lim
     if (j * kBlock + tid < nb) atomicAdd(&S.hist[w][bin(r[j])], 1);
   __syncthreads();
   if (w == 0) {  // the highest bin b with #(keys in bins >= b) >= k
-    int c[4];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
-      const int b = 255 - (4 * lane + j);
-      c[j] = S.hist[0][b] + S.hist[1][b] + S.hist[2][b] + S.hist[3][b];
-      sum += c[j];
-    }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int o = __shfl_up(incl, off);
-      if (lane >= off) incl += o;
-    }
-    int run = incl - sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (run < k && k <= run + c[j]) {
-        S.digit = 255 - (4 * lane + j);
-        S.above = run + c[j];
-      }
-      run += c[j];
-    }
+    hist_cut_bin(S.hist, k, &S.digit, &S.above);
     if (lane == 0) S.ncut = 0;
   }
   __syncthreads();
@@ -831,35 +845,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
     if (kk != 0ull) atomicAdd(&S.hist[w][bin(kk)], 1);
   }
   __syncthreads();
-  if (w == 0) {  // the highest bin b with #(keys in bins >= b) >= k; bin 0 (all) when fewer
-    int c[4];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // lane owns bins 255-4*lane-j (descending)
-      const int b = 255 - (4 * lane + j);
-      c[j] = S.hist[0][b] + S.hist[1][b] + S.hist[2][b] + S.hist[3][b];
-      sum += c[j];
-    }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int o = __shfl_up(incl, off);
-      if (lane >= off) incl += o;
-    }
-    int run = incl - sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (run < k && k <= run + c[j]) {
-        S.digit = 255 - (4 * lane + j);
-        S.above = run + c[j];
-      }
-      run += c[j];
-    }
-    if (lane == kWave - 1 && incl < k) {
-      S.digit = 0;
-      S.above = incl;
-    }
-  }
+  if (w == 0) hist_cut_bin(S.hist, k, &S.digit, &S.above);  // (bin 0, all keys, when fewer than k)
   __syncthreads();
   const int bstar = S.digit;
   if (S.above > kBlock) return false;
@@ -905,6 +891,105 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   block_sort_keys(exb, nex);
   write_keys(exb, a, q, min(nex, k));
   return true;
+}
+
+// Threshold of the int8 pre-filter from an int8 sampling pass (scan mode
+// kMaxQ8): per query, each of its cap units' largest approximate score A (lv)
+// and that row of the companion (li).  A 256-bin histogram of A over its
+// [min, max] picks the units of the fewest top bins holding >= k of them (up
+// to kBlock are kept: any k real rows will do); their rows are rescored
+// exactly, as the final select rescores (fp32 sums of the fp16 products), and
+// tau is the k-th best of those scores.  They are k real rows, so tau is at
+// most the k-th best score of the final select.  One workgroup per query; U
+// units per thread (cap <= U * kBlock).
+template <int MODE, int U>
+__global__ __launch_bounds__(kBlock) void tau_rescore_kernel(SelectArgs a) {
+  constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
+  __shared__ int hist[kWaves][256];
+  __shared__ float mm[2][kWaves];
+  __shared__ int sids[kBlock];
+  __shared__ uint64_t ex[kBlock];
+  __shared__ int nrow, nex, bstar_s, above_s;
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int w = tid / kWave;
+  const int m = a.cap;
+  const int k = a.k;
+  float av[U];
+  int row[U];
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+  const float* src = a.lv + (int64_t)q * m;
+  const int* rsrc = a.li + (int64_t)q * m;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {  // (unconditional loads, clamped: they issue together)
+    const int i = u * kBlock + tid;
+    const int ic = i < m ? i : m - 1;
+    av[u] = src[ic];
+    row[u] = rsrc[ic];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {  // a unit counts when it has a row (A > -inf, row < n)
+    const bool ok = u * kBlock + tid < m && av[u] > -__builtin_inff() && row[u] >= 0 && row[u] < a.n;
+    if (!ok) av[u] = -__builtin_inff();
+    else {
+      lo = fminf(lo, av[u]);
+      hi = fmaxf(hi, av[u]);
+    }
+  }
+  for (int i = tid; i < kWaves * 256; i += kBlock) (&hist[0][0])[i] = 0;
+  if (tid == 0) {
+    nrow = 0;
+    nex = 0;
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off));
+    hi = fmaxf(hi, __shfl_xor(hi, off));
+  }
+  if (lane == 0) {
+    mm[0][w] = lo;
+    mm[1][w] = hi;
+  }
+  __syncthreads();
+  lo = mm[0][0];
+  hi = mm[1][0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    lo = fminf(lo, mm[0][i]);
+    hi = fmaxf(hi, mm[1][i]);
+  }
+  // bin(A): non-decreasing, in [0, 255] (as block_cut_hist)
+  const bool span = hi > lo && __builtin_isfinite(lo) && __builtin_isfinite(hi);
+  const float scale = span ? 256.0f / (hi - lo) : 0.0f;
+  auto bin = [&](float v) {
+    const float t = (v - lo) * scale;
+    return (int)(t >= 0.0f ? fminf(t, 255.0f) : 0.0f);
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (av[u] > -__builtin_inff()) atomicAdd(&hist[w][bin(av[u])], 1);
+  __syncthreads();
+  if (w == 0) hist_cut_bin(hist, k, &bstar_s, &above_s);
+  __syncthreads();
+  const int bstar = bstar_s;
+  // the rows of the units in the top bins (every unit when fewer than k)
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (av[u] > -__builtin_inff() && bin(av[u]) >= bstar) {
+      const int p = atomicAdd(&nrow, 1);
+      if (p < kBlock) sids[p] = row[u];
+    }
+  }
+  __syncthreads();
+  const int mr = min(nrow, kBlock);
+  map_sids(sids, mr, a.perm);
+  half8 qv[RL];
+  load_query_pieces<RL>(a, q, qv);
+  rescore_rows<RL, RU>(ex, &nex, sids, mr, 0ull, qv, a.x, a.d);
+  __syncthreads();
+  if (mr >= k) block_rank_sort(ex, mr);  // (mr <= kBlock) the k best first
+  if (tid == 0) a.tau[q] = mr >= k ? key_score(ex[k - 1]) : -__builtin_inff();
 }
 
 // Final stage of the int8 pre-filter: the exact top-k of query blockIdx.x from
@@ -1323,6 +1408,28 @@ hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
       }
       hipLaunchKernelGGL(select_kernel<kSelTau>, dim3(nq), dim3(kBlock), 0, s, a);
       break;
+    case kSelTauRescore: {
+      if (a.q == nullptr || a.x == nullptr || a.li == nullptr || a.lv == nullptr || a.tau == nullptr || a.d < 8 ||
+          a.d % 8 != 0 || a.d > kMaxD || a.cap < 1 || a.cap > 16 * kBlock || a.k > kBlock)
+        return hipErrorInvalidValue;
+      const int u = a.cap <= 2 * kBlock ? 2 : a.cap <= 4 * kBlock ? 4 : a.cap <= 8 * kBlock ? 8 : 16;
+      const int wc = a.d <= 16 * 8 * RescoreShape<kSelRescore>::RL      ? 0
+                     : a.d <= 16 * 8 * RescoreShape<kSelRescoreMid>::RL ? 1
+                                                                         : 2;
+#define CVS_TAU_RESCORE(MODEW, UU) hipLaunchKernelGGL((tau_rescore_kernel<MODEW, UU>), dim3(nq), dim3(kBlock), 0, s, a)
+      if (wc == 0) {
+        if (u == 2) CVS_TAU_RESCORE(kSelRescore, 2); else if (u == 4) CVS_TAU_RESCORE(kSelRescore, 4);
+        else if (u == 8) CVS_TAU_RESCORE(kSelRescore, 8); else CVS_TAU_RESCORE(kSelRescore, 16);
+      } else if (wc == 1) {
+        if (u == 2) CVS_TAU_RESCORE(kSelRescoreMid, 2); else if (u == 4) CVS_TAU_RESCORE(kSelRescoreMid, 4);
+        else if (u == 8) CVS_TAU_RESCORE(kSelRescoreMid, 8); else CVS_TAU_RESCORE(kSelRescoreMid, 16);
+      } else {
+        if (u == 2) CVS_TAU_RESCORE(kSelRescoreWide, 2); else if (u == 4) CVS_TAU_RESCORE(kSelRescoreWide, 4);
+        else if (u == 8) CVS_TAU_RESCORE(kSelRescoreWide, 8); else CVS_TAU_RESCORE(kSelRescoreWide, 16);
+      }
+#undef CVS_TAU_RESCORE
+      break;
+    }
     case kSelRescore:
       if (a.q == nullptr || a.x == nullptr || a.li == nullptr || a.lcount == nullptr || a.d < 8 || a.d % 8 != 0 ||
           a.d > kMaxD || a.wave_rows < 1 || a.rsplits < 1 || a.tile_rows < a.rsplits * a.wave_rows ||

@@ -572,7 +572,8 @@ def test_q8_build_matches_oracle(eng, n, d):
 Q8_CASES = [(1, 30000, 384, 10), (7, 20000, 320, 5), (33, 25000, 384, 64), (65, 30000, 512, 10),
             (129, 20000, 768, 100), (256, 40000, 384, 10), (300, 20000, 1024, 256), (40, 20000, 1536, 1),
             # 8-wave int8 kernels with a sampled threshold and a partial last tile
-            (256, 300001, 384, 10), (200, 262193, 768, 16),
+            # (the int8 sampling pass, one unit per workgroup row split and lane group)
+            (256, 300001, 384, 10), (200, 262193, 768, 16), (256, 200003, 768, 100),
             # the 384-byte-row scan (batches above 128): a ragged last query group, d < 384
             (129, 70001, 320, 7), (255, 65536, 384, 33)]
 
