@@ -206,7 +206,7 @@ hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_q8_queries(const Q8QueryArgs& a, hipStream_t s) {
-  if (a.d < 1 || a.d > kQ8RowPer * kWave || a.dq < a.d || a.dq > kQ8RowPer * kWave || a.dq % 128 != 0)
+  if (a.d < 8 || a.d % 8 != 0 || a.d > kQ8RowPer * kWave || a.dq < a.d || a.dq > kQ8RowPer * kWave || a.dq % 128 != 0)
     return hipErrorInvalidValue;
   const int64_t per = kBlock / kWave;
   const int64_t grid = (a.nq + per - 1) / per;

@@ -16,17 +16,22 @@ __device__ __forceinline__ signed char q8_quant(float v, float inv) {
   return (signed char)fminf(127.f, fmaxf(-127.f, r));
 }
 
-// The row's elements for this lane (lane + 64 i), zero past d.
+// The row's elements for this lane: 8 consecutive ones per 512-element group
+// g, [512 g + 8 lane, 512 g + 8 lane + 8), zero past d (d % 8 == 0, the row
+// 16-byte aligned).  The three 16-byte loads are unconditional (clamped
+// inside the row), so they issue together.
 __device__ __forceinline__ void q8_load_row(const _Float16* src, int d, int lane, float (&v)[kQ8RowPer]) {
 #pragma unroll
-  for (int i = 0; i < kQ8RowPer; ++i) {
-    const int c = i * kWave + lane;
-    v[i] = c < d ? (float)src[c] : 0.f;
+  for (int g = 0; g < kQ8RowPer / 8; ++g) {
+    const int c = g * 8 * kWave + 8 * lane;
+    const half8 h = *(const half8*)(src + (c < d ? c : d - 8));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[8 * g + j] = c < d ? (float)h[j] : 0.f;
   }
 }
 
 // Whole wave, on the values q8_load_row loaded; `lane` = lane id.  dst holds
-// dq >= d bytes (zero past d).
+// dq >= d bytes (zero past d; dq % 8 == 0), written 8 bytes per lane.
 __device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int d, int dq, signed char* dst,
                                                 float4* meta, int lane) {
   constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;
@@ -40,13 +45,18 @@ __device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int
   int sq = 0;  // sum of q~^2, exact (< 1536 * 127^2)
   float ee = 0.f;
 #pragma unroll
-  for (int i = 0; i < kQ8RowPer; ++i) {
-    const int c = i * kWave + lane;
-    const signed char qc = q8_quant(v[i], inv);
-    const float e = fmaf(-s, (float)qc, v[i]);
-    sq += (int)qc * (int)qc;
-    ee = fmaf(e, e, ee);
-    if (c < dq) dst[c] = c < d ? qc : (signed char)0;
+  for (int g = 0; g < kQ8RowPer / 8; ++g) {
+    const int c = g * 8 * kWave + 8 * lane;
+    uint64_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const signed char qc = q8_quant(v[8 * g + j], inv);  // (0 past d: v is 0 there)
+      const float e = fmaf(-s, (float)qc, v[8 * g + j]);
+      sq += (int)qc * (int)qc;
+      ee = fmaf(e, e, ee);
+      packed |= (uint64_t)(uint8_t)qc << (8 * j);
+    }
+    if (c < dq) *(uint64_t*)(dst + c) = packed;
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {

@@ -1391,7 +1391,8 @@ hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
       break;
     case kSelTau:
       if (a.qq_out != nullptr &&
-          (a.q == nullptr || a.qmeta_out == nullptr || a.d < 1 || a.d > a.dq || a.dq > kQ8RowPer * kWave))
+          (a.q == nullptr || a.qmeta_out == nullptr || a.d < 8 || a.d % 8 != 0 || a.d > a.dq || a.dq % 8 != 0 ||
+           a.dq > kQ8RowPer * kWave))
         return hipErrorInvalidValue;
       if (a.nlists == 1 && a.li == nullptr && a.lcount == nullptr && a.cap >= 1 && a.cap <= 8 * kWave) {
         // one list of at most 512 unit maxima per query: the one-wave kernel
