@@ -35,10 +35,12 @@ config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
   settings of bench/bench_baselines.py:125-127); their results double as the
   recall check of the GPU output.
 
-Warm-up: after the GPU has idled (data generation) or run other work, the
-first ~25-50 searches of the C2 int8 path run 7-10% slower whatever this
-library does (measured per call: the same after 2 s idle and after a matmul
-burn, nothing at the cache-resident C1); W defaults to 20.
+Clock settling: the GPU's clocks take ~20 ms of sustained MFMA work to settle
+(measured per call after 2 s idle: the C2 search 176-199 -> 146-149 us over its
+first ~100 calls, a hipBLASLt 4096^3 fp16 GEMM 147 -> 121 us the same way, a
+384 MB device copy flat at 153-156 us).  Before its W warm-up steps each config
+therefore runs its step untimed for --settle-ms (default 30) of wall time
+(``settle_calls`` in its row); the timed region is still exactly K steps.
 """
 
 from __future__ import annotations
@@ -96,7 +98,7 @@ def end_to_end(n, d, b, k, ms, int8, dq):
     return out
 
 
-def run_config(name, steps, warmup, eng, torch, synthetic, Index):
+def run_config(name, steps, warmup, eng, torch, synthetic, Index, settle_ms=30.0):
     from cuda_vector_search.index import q8_row_bytes
 
     n, d, b, k, ties = synthetic.CONFIGS[name]
@@ -111,6 +113,13 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
     def step():
         return index.search(q, k)
 
+    settle_calls = 0  # untimed, until the clocks have settled (module docstring)
+    t_settle = time.perf_counter() + settle_ms / 1000.0
+    while settle_calls < 1 or time.perf_counter() < t_settle:
+        step()
+        settle_calls += 1
+        if settle_calls % 8 == 0:
+            torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -170,6 +179,7 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index):
     row = {
         "config": name, "n": n, "d": d, "batch": b, "k": k, "near_ties": ties,
         "plan": [int(v) for v in plan.tolist()],
+        "settle_calls": settle_calls,
         "ms_per_batch": round(wall_ms, 4), "device_ms_per_batch": round(dev_ms, 4),
         "qps": round(b / (wall_ms / 1000.0), 1),
         "path": "int8" if int8 else "fused",
@@ -379,6 +389,8 @@ def main():
                     help="untimed steps before each config's timed ones")
     ap.add_argument("--configs", default="C2,C1,C3,C4,C5",
                     help="first entry is the headline workload")
+    ap.add_argument("--settle-ms", type=float, default=30.0,
+                    help="untimed wall time of each config's step before its warm-up (clock settling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-queries", type=int, default=64,
                     help="queries of each batch in the CPU baseline's sample (all of a smaller batch)")
@@ -418,7 +430,7 @@ def main():
     cpu = None
     for i, name in enumerate(names):
         # every config gets the same warm-up and timed steps
-        row, state = run_config(name, args.steps, args.warmup, eng, torch, synthetic, Index)
+        row, state = run_config(name, args.steps, args.warmup, eng, torch, synthetic, Index, args.settle_ms)
         if not args.no_cpu_baseline:
             index, q, k, out = state
             log(f"[{name}] cpu baseline ...")
