@@ -817,6 +817,28 @@ def test_q8_edge_shapes(eng, nq, n, d, k):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nq,n,d,k", [(40, 5000, 384, 256), (200, 9000, 768, 200), (256, 70000, 384, 100)])
+def test_q8_forced_sampling_with_few_units(eng, nq, n, d, k):
+    """The int8 sampling pass forced onto small corpora (fewer sampled rows or
+    units than k leave the threshold at -inf) and at k = 100 over 70k rows: the
+    same results as without the pass and as the fused path."""
+    say(f"q8 forced sampling nq={nq} n={n} d={d} k={k}")
+    x, q = make(n, d, nq, seed=n + k + 1)
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k, flags=_ext.FLAG_FORCE_PREPASS)
+    v0, i0, _ = eng.q8_topk(qd, xd, xq, k, flags=_ext.FLAG_NO_PREPASS)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    assert torch.equal(i8, i0) and torch.equal(v8, v0)
+    np.testing.assert_allclose(v8.cpu().numpy(), v.cpu().numpy(), rtol=0, atol=2e-6)
+    same = (i8 == i).cpu().numpy()
+    assert same.all() or np.abs((v8 - v).cpu().numpy())[~same].max() < 2e-6
+    assert oracle.check_exact(q.numpy(), x.numpy(), k, v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64)) >= 0.99
+
+
+@pytest.mark.gpu
 def test_q8_zero_queries_and_rows(eng):
     """All-zero queries (scale 0) and all-zero corpus blocks: every score is 0 and
     ties order by id."""
