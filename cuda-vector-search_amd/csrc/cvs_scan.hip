@@ -273,14 +273,6 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
     if (++it_buf == NBUF) it_buf = 0;
   };
-  // The int8 pre-filter's long scans issue the prologue stages first (A/B at
-  // 1M x 768, b = 256: 3 us faster); the others once the query loads have
-  // retired (below).
-  constexpr bool EARLY = (MODE == kAppendQ8);
-  if constexpr (EARLY) {
-#pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i) issue_next();
-  }
 
   // Query fragments (B operand), resident for the whole launch.  The loads are
   // unconditional so that they issue back to back (a per-load lane mask puts
@@ -450,10 +442,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // order), which kept the first tile behind the last prologue stage instead
   // of the first (C1: 38.1 -> 37.5 us per search, C5 69.3 -> 68.5 us).
   wait_vmcnt<0>();
-  if constexpr (!EARLY) {
 #pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i) issue_next();
-  }
+  for (int i = 0; i < NBUF - 1; ++i) issue_next();
 
   // The thresholds from sampling maxima: the threshold select's bit search
   // (count the maxima >= each candidate, summed over the 8 lanes by DPP),
