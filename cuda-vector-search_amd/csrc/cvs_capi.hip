@@ -917,6 +917,12 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
       P.s8_units = wgs * (P.s8_agg ? 1 : P.s8_spt) * upt;
     }
   }
+  if (P.gemv && P.sample.prepass && P.sample.units <= 16 * 256) {
+    // batch 1: the fp16 GEMV sample's blocks and units, over the int8 companion
+    P.s8 = true;
+    P.s8_nsample = P.sample.nsample;
+    P.s8_units = P.sample.units;
+  }
   P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
   if (P.groups * P.chunks > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
   const int64_t nqq = std::max<int64_t>(nq, 1);
@@ -1004,7 +1010,41 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     e = launch_q8_queries(qa, s);
     if (e != hipSuccess) return hip_fail(e, "query quantisation launch");
   }
-  if (P.s8) {  // int8 sampling pass; the threshold from rescoring its best units' rows
+  if (P.s8 && P.gemv) {  // the int8 GEMV sampling pass; the threshold as below
+    GemvArgs pg{};
+    pg.q = reinterpret_cast<const _Float16*>(qq);
+    pg.x = static_cast<const _Float16*>(xq);
+    pg.n = n;
+    pg.d = (int)P.dq;  // int8 row bytes
+    pg.k = (int)k;
+    pg.mode = kMaxQ8;
+    pg.umax = umax;
+    pg.uarg = reinterpret_cast<int*>(ws + P.off_uarg);
+    pg.nsample = (int)P.s8_nsample;
+    pg.upb = S.upb;
+    pg.units = (int)P.s8_units;
+    pg.qmeta = qm;
+    pg.bmeta = bmeta;
+    pg.gamma = gamma;
+    e = launch_gemv(pg, (int)ceil_div(P.s8_nsample, 4), s);
+    if (e != hipSuccess) return hip_fail(e, "int8 gemv sample pass launch");
+    SelectArgs ta{};
+    ta.lv = umax;
+    ta.li = pg.uarg;
+    ta.nlists = 1;
+    ta.cap = (int)P.s8_units;
+    ta.k = (int)k;
+    ta.tau = tau;
+    ta.q = qh;
+    ta.x = xh;
+    ta.n = n;
+    ta.d = (int)d;
+    ta.perm = perm;
+    mark(1);
+    e = launch_select(5, ta, (int)nq, s);
+    if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+    mark(2);
+  } else if (P.s8) {  // int8 sampling pass; the threshold from rescoring its best units' rows
     ScanArgs pa{};
     pa.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
     pa.x = static_cast<const _Float16*>(xq);

@@ -14,6 +14,8 @@
 // (v_dot4_i32_i8, exact int32 sums, 128-byte pieces of 128 int8): rows whose
 // score upper bound reaches the threshold are appended, a full list is marked
 // overflowed instead of compacted, and the select recomputes exact scores.
+// kMaxQ8 samples that way: per unit the largest approximate score
+// A = s_q s_b sum(q~ x~) and its row, for the threshold kernel to rescore.
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 
@@ -49,8 +51,9 @@ constexpr int kWide = 8;
 
 template <int PMAX, int MODE>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
-  constexpr bool Q8 = (MODE == kAppendQ8);
-  constexpr bool APP = (MODE == kAppend || Q8);
+  constexpr bool Q8 = (MODE == kAppendQ8 || MODE == kMaxQ8);
+  constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8);
+  constexpr bool SMAX = (MODE == kMax || MODE == kMaxQ8);
   __shared__ uint64_t sortbuf[MODE == kAppend ? 4 * kMaxCap : 1];
   const int lane = lane_id();
   const int w = threadIdx.x >> 6;
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
   if (Q8) qm = a.qmeta[0];
 
   int64_t r_begin, r_end;
-  if (MODE == kMax) {
+  if (SMAX) {
     if (gw >= a.nsample) return;  // whole wave
     const int64_t nblocks = (n + 63) / 64;
     const int64_t blk = ((2 * (int64_t)gw + 1) * nblocks) / (2 * (int64_t)a.nsample);
@@ -88,6 +91,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
 
   float thr = (APP && a.tau) ? a.tau[0] : -__builtin_inff();
   float umax = -__builtin_inff();  // kMax: best score of this lane group's rows
+  int uarg = 0;                    // kMaxQ8: its row
   int count = 0;
   float* lv = nullptr;
   int* li = nullptr;
@@ -153,7 +157,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
         ia += __shfl_xor(ia, 1);
         ia += __shfl_xor(ia, 2);
         ia += __shfl_xor(ia, 4);
-        acc = fmaf((float)ia, cq, slack);  // upper bound of the exact score
+        // upper bound of the exact score (kMaxQ8: the approximate score itself)
+        acc = MODE == kMaxQ8 ? (float)ia * cq : fmaf((float)ia, cq, slack);
       } else {
         if (WIDE) acc = wacc[u];
 #pragma unroll
@@ -167,6 +172,11 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       const bool valid = row < r_end;
       if (MODE == kMax) {
         if (valid) umax = fmaxf(umax, acc);
+      } else if (MODE == kMaxQ8) {
+        if (valid && acc > umax) {
+          umax = acc;
+          uarg = (int)row;
+        }
       } else {
         bool pass = valid && sub == 0 && acc >= thr;
         uint64_t mask = __ballot(pass);
@@ -210,6 +220,26 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvArgs a) {
       a.umax[(int64_t)gw * 8 + rg] = umax;
     }
   }
+  if (MODE == kMaxQ8) {  // the same units, each with its row (the first on ties)
+    if (a.upb == 1) {
+#pragma unroll
+      for (int off = 8; off < kWave; off <<= 1) {
+        const float om = __shfl_xor(umax, off);
+        const int oa = __shfl_xor(uarg, off);
+        if (om > umax || (om == umax && oa < uarg)) {
+          umax = om;
+          uarg = oa;
+        }
+      }
+      if (lane == 0) {
+        a.umax[gw] = umax;
+        a.uarg[gw] = uarg;
+      }
+    } else if (sub == 0) {
+      a.umax[(int64_t)gw * 8 + rg] = umax;
+      a.uarg[(int64_t)gw * 8 + rg] = uarg;
+    }
+  }
   if (APP && lane == 0) a.lcount[gw] = count;
 }
 
@@ -226,15 +256,22 @@ hipError_t launch_p(const GemvArgs& a, int grid, hipStream_t s) {
 
 template <int PMAX>
 hipError_t launch_q8(const GemvArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_kernel<PMAX, kAppendQ8>), dim3(grid), dim3(kBlock), 0, s, a);
+  if (a.mode == kMaxQ8)
+    hipLaunchKernelGGL((gemv_kernel<PMAX, kMaxQ8>), dim3(grid), dim3(kBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemv_kernel<PMAX, kAppendQ8>), dim3(grid), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_gemv(const GemvArgs& a, int grid, hipStream_t s) {
-  if (a.mode == kAppendQ8) {  // d = int8 row bytes
-    if (a.qmeta == nullptr || a.bmeta == nullptr || a.rows_per_wave % 16 != 0) return hipErrorInvalidValue;
+  if (a.mode == kAppendQ8 || a.mode == kMaxQ8) {  // d = int8 row bytes
+    if (a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
+    if (a.mode == kAppendQ8 && a.rows_per_wave % 16 != 0) return hipErrorInvalidValue;
+    if (a.mode == kMaxQ8 && (a.umax == nullptr || a.uarg == nullptr || a.nsample < 1 || (a.upb != 1 && a.upb != 8) ||
+                             a.units != a.nsample * a.upb))
+      return hipErrorInvalidValue;
     if (a.d == 384) return launch_q8<3>(a, grid, s);
     if (a.d == 768) return launch_q8<6>(a, grid, s);
     if (a.d == 1536) return launch_q8<12>(a, grid, s);

@@ -80,10 +80,11 @@ struct GemvArgs {
   int cap;
   int k;
   float* umax;        // kMax: [units], upb per sampled 64-row block
+  int* uarg;          // kMaxQ8: [units] the (companion) row of each unit's maximum
   int nsample;        // kMax: sampled 64-row blocks (one per wave)
   int upb;            // kMax: units per block, 8 (rows mod 8) or 1 (the block)
   int units;
-  int mode;           // kAppend, kMax or kAppendQ8
+  int mode;           // kAppend, kMax, kAppendQ8 or kMaxQ8 (the largest approximate score, int8)
   // kAppendQ8: q and x are int8 rows of d bytes (d = 384, 768 or 1536); the
   // filter uses the score upper bound as the scan's kAppendQ8 does
   const float4* qmeta;  // [1]

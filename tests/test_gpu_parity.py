@@ -575,7 +575,9 @@ Q8_CASES = [(1, 30000, 384, 10), (7, 20000, 320, 5), (33, 25000, 384, 64), (65, 
             # (the int8 sampling pass, one unit per workgroup row split and lane group)
             (256, 300001, 384, 10), (200, 262193, 768, 16), (256, 200003, 768, 100),
             # the 384-byte-row scan (batches above 128): a ragged last query group, d < 384
-            (129, 70001, 320, 7), (255, 65536, 384, 33)]
+            (129, 70001, 320, 7), (255, 65536, 384, 33),
+            # batch 1: the int8 GEMV sampling pass, whole-block units and 8 per block
+            (1, 200003, 768, 3), (1, 100000, 1536, 256), (1, 64000, 384, 100)]
 
 
 @pytest.mark.gpu
