@@ -273,6 +273,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
     if (++it_buf == NBUF) it_buf = 0;
   };
+  issue_next();  // stage 0 first: its latency overlaps the query loads'
 
   // Query fragments (B operand), resident for the whole launch.  The loads are
   // unconditional so that they issue back to back (a per-load lane mask puts
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int ks = 0; ks < KSMAX; ++ks) qf[qb][ks] = PIN_Q ? pin_agpr(ld[qb][ks]) : ld[qb][ks];
+      for (int ks = 0; ks < KSMAX; ++ks) qf[qb][ks] = ld[qb][ks];  // pinned after the prologue wait
   }
 
   float thr[QB];
@@ -434,16 +435,26 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
 
-  // Retire the query/threshold loads before the loop (otherwise the compiler's
-  // wait-count analysis carries them around the loop back-edge and waits on
-  // vmcnt(0) at every stage), and only then issue the prologue stages: a load
-  // the compiler tracks, waited on after the stage loads were issued, would
-  // wait for all of them too (vmcnt counts every vector memory load in issue
-  // order), which kept the first tile behind the last prologue stage instead
-  // of the first (C1: 38.1 -> 37.5 us per search, C5 69.3 -> 68.5 us).
+  // Retire the query/threshold loads (and stage 0, issued before them) with one
+  // wait before the loop (otherwise the compiler's wait-count analysis carries
+  // them around the loop back-edge and waits on vmcnt(0) at every stage), and
+  // only then issue the other prologue stages: a load the compiler tracks,
+  // waited on after stage loads were issued, would wait for all of them too
+  // (vmcnt counts every vector memory load in issue order), which kept the
+  // first tile behind the last prologue stage instead of the first (C1: 38.1 ->
+  // 37.5 us per search, C5 69.3 -> 68.5 us).  The query fragments are pinned to
+  // AGPRs only here: pinning uses a fragment, so before the wait it put a wait
+  // per fragment ahead of the loads that follow them, a second round trip
+  // (C5 66.4 -> 65.1 us, C2 -0.3 us).
   wait_vmcnt<0>();
+  if constexpr (!QL && PIN_Q) {
 #pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i) issue_next();
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < KSMAX; ++ks) qf[qb][ks] = pin_agpr(qf[qb][ks]);
+  }
+#pragma unroll
+  for (int i = 1; i < NBUF - 1; ++i) issue_next();
 
   // The thresholds from sampling maxima: the threshold select's bit search
   // (count the maxima >= each candidate, summed over the 8 lanes by DPP),
