@@ -117,6 +117,28 @@ __device__ __forceinline__ void dma_to_lds_16(const void* src, const void* lds_b
         : "memory");
 }
 
+// 16 bytes per lane from sbase + voff (lane's own offset) into LDS at
+// lds + 16 * lane.  `sbase` and `lds` must be wave-uniform.  Non-temporal: the
+// companion is streamed once per search.
+__device__ __forceinline__ void dma16_saddr(uint32_t voff, const void* sbase, uint32_t lds) {
+  // (readfirstlane returns int: each half goes through uint32_t, so the low
+  // half is zero-extended, never sign-extended into the high half)
+  const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds);
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m), "v"(voff), "s"(sb)
+      : "memory");
+}
+
 // ---- register placement -----------------------------------------------------
 
 // Returns `v` materialised in accumulation registers (AGPRs).  MFMA source

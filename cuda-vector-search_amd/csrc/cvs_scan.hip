@@ -127,14 +127,16 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int RW = MS * RB;        // rows per wave per tile
   constexpr int TR = RS * RW;        // tile rows
   constexpr int KSL = 64 / M::KSZ;   // MFMA k-steps per 128-byte line of a row
-  // TS (whole-tile stages): when a full-width tile is 24 KB (the int8 scan of
-  // 384-byte rows, 64 rows, 8 waves), a stage is the whole tile, LPR 128-byte
-  // lines per row, and every 1 KB DMA load reads 8 consecutive lines of global
-  // memory (measured: HBM -> LDS at 6.5 TB/s against 5.4 TB/s for stages of one
-  // 128-byte line per row, whose loads read 8 lines a row apart).  Otherwise a
-  // stage is one line (64 columns) of every row of the tile.
-  constexpr bool TS = FULLW && Q8 && NW == 8 && TR * KSMAX * M::KSZ * 2 == 24 * 1024;
-  constexpr int LPR = TS ? KSMAX / KSL : 1;  // lines per row in a stage
+  // TS (24 KB stages of the 8-wave int8 scans, 64-row tiles of 3k 128-byte
+  // lines per row): a stage is 3 lines of every row of the tile (the whole
+  // tile for 384-byte rows, half of it for 768-byte rows), and every 1 KB DMA
+  // load reads 8 stage lines, runs of up to 384 consecutive bytes of global
+  // memory (measured: HBM -> LDS at 6.5 TB/s against 5.4 TB/s for stages of
+  // one 128-byte line per row, whose loads read 8 lines a row apart; the
+  // 768-byte-row scan of C4 253.6 -> 237.0 us with two barriers per tile
+  // instead of six).  Otherwise a stage is one line (64 columns) of every row.
+  constexpr bool TS = FULLW && Q8 && NW == 8 && TR == 64 && (KSMAX / KSL) % 3 == 0;
+  constexpr int LPR = TS ? 3 : 1;  // lines per row in a stage
   constexpr int KPS = LPR * KSL;     // MFMA k-steps per stage
   constexpr int TRB = TR / MS;       // MS-row blocks per tile
   constexpr int FC = TR * LPR / 8;   // 1 KB DMA loads (8 lines of 128 bytes) of corpus rows per stage
@@ -250,14 +252,43 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       src[j] = a.x + src_row[j] * d + poff[j];
     }
   }
+  // TS: the int8 companion holds whole 64-row blocks, so a tile's rows are
+  // TR * row-bytes contiguous bytes that all exist (rows past n are padding,
+  // never reported): each load is a scalar tile base plus a constant lane
+  // offset, without the per-load address registers and clamps below.
+  uint32_t voff_ts[TS ? LPW : 1];
+  if constexpr (TS) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int L = (w + NW * j) * 8 + (lane >> 3);
+      const int rl = L / LPR;
+      voff_ts[j] = (uint32_t)(rl * 2 * d + (L % LPR) * 128 + (((lane & 7) ^ piece_swz(rl)) << 4));
+    }
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
   auto issue_next = [&]() {
+    if constexpr (TS) {
+      const int64_t tt = it_t < a.ntiles ? it_t : a.ntiles - 1;
+      const unsigned char* base =
+          reinterpret_cast<const unsigned char*>(a.x) + tt * (TR * 2 * (int64_t)d) + it_c * (LPR * 128);
+      const uint32_t lds = lds0 + (uint32_t)(it_buf * STAGE + w * 1024);
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) dma16_saddr(voff_ts[j], base, lds + (uint32_t)(j * NW * 1024));
+      if (++it_c == nc) {
+        it_c = 0;
+        ++it_t;
+      }
+      if (++it_buf == NBUF) it_buf = 0;
+      return;
+    }
     unsigned char* buf = smem + it_buf * STAGE;
     const bool whole = (it_t + 1) * TR <= n;  // every row of this tile exists
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int f = w + NW * j;
-      const _Float16* p = src[j] + it_c * 64;
-      if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * 64 + poff[j];
+      const _Float16* p = src[j] + it_c * (64 * LPR);
+      if (!whole && src_row[j] >= n) p = a.x + (n - 1) * d + it_c * (64 * LPR) + poff[j];
       dma_to_lds_16<Q8>(p, buf + f * 1024);
     }
     if (++it_c == nc) {
@@ -506,18 +537,21 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   // line kk / KSL, piece (kk % KSL)*G + kg, at (R*LPR + line)*128 +
   // ((piece ^ piece_swz(R)) << 4); piece_swz(R) depends on R mod 16 = col mod
   // 16 only, so one lane offset per k-step serves every rb.
-  int aoff[KPS];
+  // (one lane offset per piece of a line; the line's 128-byte step is an
+  // immediate offset of the read)
+  int aoff[KSL];
 #pragma unroll
-  for (int kk = 0; kk < KPS; ++kk)
-    aoff[kk] = ((rs * RB * MS + col) * LPR + kk / KSL) * 128 + ((((kk % KSL) * G + kg) ^ piece_swz(col)) << 4);
+  for (int kk = 0; kk < KSL; ++kk)
+    aoff[kk] = (rs * RB * MS + col) * LPR * 128 + (((kk * G + kg) ^ piece_swz(col)) << 4);
   constexpr int RBOFF = MS * LPR * 128;  // LDS bytes between row blocks
+  auto a_at = [&](int kk) { return aoff[kk % KSL] + (kk / KSL) * 128; };
   auto read_stage = [&](int buf_idx, half8 (&f)[KPS][RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
     for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
-        f[kk][rb] = *(const half8*)(buf + aoff[kk] + rb * RBOFF);
+        f[kk][rb] = *(const half8*)(buf + a_at(kk) + rb * RBOFF);
   };
   // QL: B fragment of k-step kk, query block qb: query-area row
   // Rq = qs*QW + qb*MS + col (after the TR corpus rows), same piece rule.
@@ -549,7 +583,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   auto read_ks = [&](int buf_idx, int kk, half8 (&f)[RB]) {
     const unsigned char* buf = smem + buf_idx * STAGE;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + aoff[kk] + rb * RBOFF);
+    for (int rb = 0; rb < RB; ++rb) f[rb] = *(const half8*)(buf + a_at(kk) + rb * RBOFF);
   };
   wait_vmcnt_lgkm0<(NBUF - 2) * LPW>();  // first stage landed (this wave)
   __builtin_amdgcn_s_barrier();           // ... and for every wave
