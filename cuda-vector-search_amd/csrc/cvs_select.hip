@@ -752,7 +752,7 @@ __device__ __forceinline__ void rescore_rows(uint64_t* out, int* cnt, const int*
 // whose U reaches score(kappa) is rescored at once (a candidate below it has
 // S' <= U < score(kappa) and cannot enter).  The same rows' exact keys as the
 // general path below, so the same top k.  Returns false, having written
-// nothing, when the top bins hold more than kBlock keys or the second round
+// nothing, when the top bins hold more than kBlock keys or the second rescoring pass
 // more than kBuf - k rows (many equal bounds); the general path then runs.
 // Whole block.
 template <int RL, int RU>
@@ -781,7 +781,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   // line); of a few hundred, all are, on the way (saving map_sids' round trips).
   const bool map_now = total <= 1024;
   // the list of every entry, written by the list's thread into sids (free
-  // until round 1): one LDS read per entry instead of a binary search
+  // until the first rescoring pass): one LDS read per entry instead of a binary search
   for (int L = tid; L < NL; L += kBlock)
     for (int i = S.pre[L], e = S.pre[L + 1]; i < e; ++i) sids[i] = L;
   __syncthreads();
@@ -849,7 +849,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   __syncthreads();
   const int bstar = S.digit;
   if (S.above > kBlock) return false;
-  // round 1: the top bins' rows
+  // first rescoring pass: the top bins' rows
   for (int i = tid; i < total; i += kBlock) {
     const uint64_t kk = cand(i);
     if (kk != 0ull && bin(kk) >= bstar) sids[atomicAdd(&cnt[1], 1)] = key_id(kk);
@@ -861,7 +861,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   load_query_pieces<RL>(a, q, qv);
   rescore_rows<RL, RU>(ex1, &cnt[0], sids, m1, 0ull, qv, a.x, a.d);
   __syncthreads();
-  uint64_t kap = 0ull;  // k-th best exact key of round 1 (0: fewer than k rows in all)
+  uint64_t kap = 0ull;  // k-th best exact key of the first pass (0: fewer than k rows in all)
   if (m1 > k) {
     block_rank_sort(ex1, m1);  // m1 <= kBlock; the k best first
     kap = ex1[k - 1];
@@ -871,7 +871,7 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
   const int k1 = min(m1, k);
   if (tid == 0) cnt[1] = 0;
   __syncthreads();
-  // round 2: every other row whose bound reaches score(kappa)
+  // second rescoring pass: every other row whose bound reaches score(kappa)
   if (kap != 0ull) {
     const float umin = key_score(kap);
     for (int i = tid; i < total; i += kBlock) {
@@ -1018,7 +1018,7 @@ __global__ __launch_bounds__(kBlock) void rescore_select_kernel(SelectArgs a) {
   constexpr int RL = RescoreShape<MODE>::RL, RU = RescoreShape<MODE>::RU;
   __shared__ int sids[2 * kBuf];                  // rows to rescore
   __shared__ uint64_t ex[kBuf];                   // one-pass form: candidates past kBuf, then exact keys
-  __shared__ uint64_t ex1[kBlock];                // one-pass form: round 1's exact keys
+  __shared__ uint64_t ex1[kBlock];                // one-pass form: exact keys of the first rescoring pass
   __shared__ unsigned ovf[kSelectMaxLists / 32];  // overflowed-list bitmap
   __shared__ uint64_t red[kWaves];
   __shared__ int nrows;
