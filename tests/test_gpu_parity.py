@@ -599,6 +599,43 @@ def test_q8_topk_matches_fused(eng, nq, n, d, k):
     assert same.mean() > 0.999 or np.abs(v8 - v)[~same].max() < 2e-6
 
 
+def _random_q8_cases(count=16, seed=20261202):
+    """Seeded random (nq, n, d, k): widths 64-1536, batches 1-300 (the batch-1
+    GEMV, the 4- and 8-wave scans, the 384-byte-row scan), corpora with partial
+    last tiles, k 1-256; nq * n * d bounded so the oracle check takes seconds."""
+    rng = np.random.default_rng(seed)
+    widths = [64, 128, 192, 256, 320, 384, 448, 512, 640, 768, 896, 1024, 1536]
+    batches = [1, 1, 2, 5, 17, 64, 100, 129, 200, 256, 300]
+    out = []
+    while len(out) < count:
+        d = int(rng.choice(widths))
+        nq = int(rng.choice(batches))
+        n = int(np.exp(rng.uniform(np.log(2000), np.log(250000))))  # log-uniform
+        if nq * n * d > 4e9:
+            continue
+        k = int(min(n, rng.choice([1, 3, 10, 32, 64, 100, 200, 256])))
+        out.append((nq, n, d, k))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nq,n,d,k", _random_q8_cases())
+def test_q8_random_shapes_match_fused_and_oracle(eng, nq, n, d, k):
+    say(f"q8 random nq={nq} n={n} d={d} k={k}")
+    x, q = make(n, d, nq, seed=nq * 7919 + n + d + k)
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    v8, i8, v, i = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64), v.cpu().numpy(), i.cpu().numpy()
+    assert oracle.check_exact(q.numpy(), x.numpy(), k, v8, i8) >= 0.99
+    np.testing.assert_allclose(v8, v, rtol=0, atol=2e-6)
+    same = (i8 == i)
+    assert same.mean() > 0.999 or np.abs(v8 - v)[~same].max() < 2e-6
+
+
 @pytest.mark.gpu
 def test_q8_overflowing_lists_are_rescanned(eng):
     """4000 copies of the best row: every copy passes the int8 bound, the
