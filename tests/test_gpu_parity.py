@@ -126,6 +126,32 @@ def test_fused_matches_exact(eng, n, d, b, k):
     assert rec >= 0.999
 
 
+def _random_fused_cases(count=16, seed=20261203):
+    """Seeded random (nq, n, d, k) for the fp16 path: widths 8-4096 (zero-padded
+    to multiples of 64; the wide path above 1536), batches 1-300 (the batch-1
+    GEMV and every query-block size), log-uniform corpus sizes, k 1-256."""
+    rng = np.random.default_rng(seed)
+    batches = [1, 1, 3, 16, 17, 32, 64, 65, 128, 200, 256, 300]
+    out = []
+    while len(out) < count:
+        d = int(rng.choice([int(rng.integers(1, 64)) * 8, int(rng.integers(1, 25)) * 64, int(rng.integers(25, 65)) * 64]))
+        nq = int(rng.choice(batches))
+        n = int(np.exp(rng.uniform(np.log(500), np.log(200000))))
+        if nq * n * d > 4e9:
+            continue
+        k = int(min(n, rng.choice([1, 5, 10, 50, 100, 256])))
+        out.append((nq, n, d, k))
+    return out
+
+
+@pytest.mark.parametrize("nq,n,d,k", _random_fused_cases())
+def test_fused_random_shapes_match_oracle(eng, nq, n, d, k):
+    say(f"fused random nq={nq} n={n} d={d} k={k}")
+    x, q = make(n, d, nq, seed=nq * 104729 + n + d + k)
+    v, i, _ = run_fused(eng, q, x, k)
+    oracle.check_exact(q.numpy(), x.numpy(), k, v, i)
+
+
 @pytest.mark.parametrize("n,d,b,k", [(5000, 384, 8, 10), (20000, 768, 64, 100)])
 def test_twopass_and_torch_paths(eng, n, d, b, k):
     say(f"twopass/torch n={n} d={d} b={b} k={k}")
