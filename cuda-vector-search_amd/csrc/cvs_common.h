@@ -31,6 +31,15 @@ __device__ __forceinline__ float order_float(uint32_t o) {
   return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
+// The threshold for an order key found by a bit search truncated above its low
+// bits: order_float(t), except that keys below float_order(-FLT_MAX) (those of
+// -inf and of the NaNs past it, which a truncated search reaches when the k-th
+// largest maximum is -inf) give -inf, a threshold every score passes.  A NaN
+// threshold would pass none.
+__device__ __forceinline__ float order_threshold(uint32_t t) {
+  return t < 0x00800000u ? -__builtin_inff() : order_float(t);
+}
+
 __device__ __forceinline__ uint64_t make_key(float v, int id) {
   return ((uint64_t)float_order(v) << 32) | (uint64_t)(~(uint32_t)id);
 }

@@ -169,7 +169,9 @@ __global__ __launch_bounds__(kBlock) void q8_query_kernel(Q8QueryArgs a) {
 }  // namespace
 
 // Row order, then the blocks.  The sort's key and id buffers and its scratch
-// are one stream-ordered allocation, released on the stream after the sort.
+// live in the companion's own int8-row region (rows * dq >= 384 n bytes, far
+// more than the ~14 n bytes they take), which q8_build_kernel overwrites only
+// after the sort, in stream order: the build allocates nothing.
 hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
   if (a.d < 8 || a.d % 8 != 0 || a.dq < a.d || a.dq % 128 != 0 || a.perm == nullptr) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + 63) / 64;
@@ -181,9 +183,8 @@ hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   const size_t keys_bytes = ((size_t)n * sizeof(uint16_t) + 255) / 256 * 256;
   const size_t ids_bytes = ((size_t)n * sizeof(int) + 255) / 256 * 256;
-  char* buf = nullptr;
-  e = hipMallocAsync(reinterpret_cast<void**>(&buf), 2 * keys_bytes + ids_bytes + sort_bytes, s);
-  if (e != hipSuccess) return e;
+  if (2 * keys_bytes + ids_bytes + sort_bytes > (size_t)rows * (size_t)a.dq) return hipErrorInvalidValue;
+  char* buf = reinterpret_cast<char*>(a.xq);
   uint16_t* key_in = reinterpret_cast<uint16_t*>(buf);
   uint16_t* key_out = reinterpret_cast<uint16_t*>(buf + keys_bytes);
   int* ids = reinterpret_cast<int*>(buf + 2 * keys_bytes);
@@ -192,11 +193,9 @@ hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(q8_rowkey_kernel, dim3((unsigned)((n + per - 1) / per)), dim3(kBlock), 0, s, a.x, n, a.d,
                      key_in, ids);
   e = hipGetLastError();
-  if (e == hipSuccess)
-    e = rocprim::radix_sort_pairs(tmp, sort_bytes, key_in, key_out, ids, a.perm, (unsigned)n, 0, 15, s);
-  const hipError_t ef = hipFreeAsync(buf, s);
   if (e != hipSuccess) return e;
-  if (ef != hipSuccess) return ef;
+  e = rocprim::radix_sort_pairs(tmp, sort_bytes, key_in, key_out, ids, a.perm, (unsigned)n, 0, 15, s);
+  if (e != hipSuccess) return e;
   if (rows > n)
     hipLaunchKernelGGL(q8_perm_pad_kernel, dim3((unsigned)((rows - n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s,
                        a.perm, n, rows);

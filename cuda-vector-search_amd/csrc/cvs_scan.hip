@@ -524,7 +524,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
           if (sum8_i32(c) >= a.k) tk = cand;
         }
       }
-      const float tv = qi >= a.nq ? __builtin_inff() : (a.units_in >= a.k ? order_float(tk) : -__builtin_inff());
+      const float tv = qi >= a.nq ? __builtin_inff() : (a.units_in >= a.k ? order_threshold(tk) : -__builtin_inff());
       if (g8 == 0)
 #pragma unroll
         for (int r = 0; r < RS; ++r) thr_s[r][ql] = tv;

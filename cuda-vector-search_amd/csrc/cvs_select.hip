@@ -629,7 +629,7 @@ __global__ __launch_bounds__(kWave) void tau_kernel(SelectArgs a) {
       if (c >= a.k) t = cand;
     }
   }
-  if (lane == 0) a.tau[q] = (m >= a.k) ? order_float(t) : -__builtin_inff();
+  if (lane == 0) a.tau[q] = (m >= a.k) ? order_threshold(t) : -__builtin_inff();
   if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane);
 }
 
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(kBlock) void tau_block_kernel(SelectArgs a) {
       if (tot >= a.k) t = cand;
     }
   }
-  if (tid == 0) a.tau[q] = (m >= a.k) ? order_float(t) : -__builtin_inff();
+  if (tid == 0) a.tau[q] = (m >= a.k) ? order_threshold(t) : -__builtin_inff();
   if (a.qq_out != nullptr && w == 0) {
     float qrow[kQ8RowPer];
     q8_load_row(a.q + (int64_t)q * a.d, a.d, lane, qrow);

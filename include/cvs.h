@@ -193,8 +193,9 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
  *   (256-byte aligned, at least cvs_q8_corpus_bytes): the rows in ascending
  *   order of their largest magnitude (stable), so that each 64-row block, which
  *   shares one int8 scale, holds rows of nearly equal range.  Rebuild it
- *   whenever x changes.  The call allocates (and releases, stream-ordered) a
- *   scratch buffer of about 8 bytes per row for the sort.
+ *   whenever x changes.  The row-order sort's keys, ids and scratch (about 14
+ *   bytes per row) are placed in xq's own int8-row region before the rows
+ *   are written, so the call allocates nothing.
  * cvs_q8_plan / cvs_q8_topk: as cvs_fused_plan / cvs_fused_topk (1 <= k <= 256,
  *   auto plan only; flags CVS_FLAG_IDS_INT64, and the pre-pass flags for the
  *   sampling pass), with the companion of x as xq.  plan_out[0] is the int8

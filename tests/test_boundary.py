@@ -52,6 +52,20 @@ def test_library_exports_every_declared_symbol(lib_path):
     assert not missing, f"declared in cvs.h but not exported: {missing}"
 
 
+def test_library_imports_no_allocation_call(lib_path):
+    """No entry point allocates or frees device or host memory through HIP:
+    outputs and workspaces are the caller's, and the int8 companion build sorts
+    inside the buffer it is given."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(lib_path)], capture_output=True,
+                         text=True, check=True).stdout
+    imported = {s.split("@")[0] for s in re.findall(r"\bU\s+(\S+)", out)}
+    assert "hipLaunchKernel" in imported or any(s.startswith("__hipRegister") for s in imported)
+    alloc = sorted(s for s in imported if re.match(r"hip(Ext)?(Malloc|Free|HostAlloc|HostMalloc|HostFree|"
+                                                   r"MallocAsync|FreeAsync|MemPool|MallocManaged|"
+                                                   r"MallocPitch|Malloc3D|MallocArray)", s))
+    assert not alloc, f"libcvs_hip.so imports allocation calls: {alloc}"
+
+
 def test_library_is_gfx950_code(lib_path):
     # the embedded offload bundle names its target triple; nothing else may be there
     blob = lib_path.read_bytes()

@@ -273,6 +273,31 @@ def test_prepass_does_not_change_results(eng, flags, n, d, b, k):
     np.testing.assert_array_equal(i, i0)
 
 
+@pytest.mark.parametrize("n,d,b,k", [(100, 384, 5, 28), (65, 384, 3, 20), (65, 128, 3, 20), (100, 768, 5, 28),
+                                     (130, 256, 40, 60), (70, 384, 200, 40)])
+def test_forced_prepass_with_fewer_finite_units_than_k(eng, n, d, b, k):
+    """A forced sampling pass over a corpus whose last tile is mostly past n:
+    the sampled units outnumber k, but fewer than k of them hold a row (the
+    rest are -inf), so the k-th largest maximum is -inf.  The truncated bit
+    search of the threshold must then give -inf (every row a candidate), not
+    a threshold no score reaches."""
+    say(f"forced prepass, few finite units n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=n + k)
+    v, i, _ = run_fused(eng, q, x, k, flags=_ext.FLAG_FORCE_PREPASS)
+    oracle.check_exact(q, x, k, v, i)
+    v0, i0, _ = run_fused(eng, q, x, k, flags=_ext.FLAG_NO_PREPASS)
+    np.testing.assert_array_equal(v, v0)
+    np.testing.assert_array_equal(i, i0)
+    qd = pad64(q).cuda().contiguous()
+    xd = pad64(x).cuda().contiguous()
+    v8, i8, _ = eng.q8_topk(qd, xd, eng.q8_build(xd), k, flags=_ext.FLAG_FORCE_PREPASS)
+    torch.cuda.synchronize()
+    v8, i8 = v8.cpu().numpy(), i8.cpu().numpy().astype(np.int64)
+    np.testing.assert_allclose(v8, v, rtol=0, atol=2e-6)
+    same = i8 == i
+    assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
+
+
 @pytest.mark.parametrize("k", [10, 100])
 def test_two_group_sampling_on_paired_xcds(eng, k):
     """d = 768 at b = 256 runs two 128-query groups; with 128 sampling
