@@ -841,8 +841,11 @@ struct Q8Plan {
   bool s8 = false;
   int64_t s8_nsample = 0, s8_spt = 1, s8_units = 0;
   int s8_agg = 0;
-  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_uarg = 0, off_qq = 0, off_qm = 0,
-          ws_bytes = 0;
+  // the lean 384-byte-row int8 scan (q8scan384_kernel), and whether it takes
+  // the thresholds itself (tau_in_scan) instead of a threshold launch
+  bool lean = false, tau_in_scan = false;
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_tauw = 0, off_umax = 0, off_uarg = 0, off_qq = 0,
+          off_qm = 0, ws_bytes = 0;
 };
 
 int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus, Q8Plan* out) {
@@ -925,6 +928,17 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   }
   P.cap = std::max<int64_t>(128, pow2_at_least(k + 64));
   if (P.groups * P.chunks > INT_MAX) return fail(CVS_ERR_INVALID, "too many queries");
+  if (!P.gemv) {
+    const ScanCfg c384{32, 8, 1, 2, 12};
+    P.lean = P.cfg.ms == c384.ms && P.cfg.qs == c384.qs && P.cfg.qb == c384.qb && P.cfg.rb == c384.rb &&
+             P.cfg.ksmax == c384.ksmax && P.dq == 384 && P.nlists == P.chunks;
+    // In-scan thresholds: workgroup b computes that of query b (the grid
+    // extends past the chunks to one workgroup per query), and every
+    // workgroup waits for its queries', so the whole grid must be resident at
+    // once (one 8-wave workgroup per CU).
+    P.tau_in_scan = P.lean && P.s8 && !(flags & CVS_FLAG_TAU_LAUNCH) && P.groups == 1 &&
+                    std::max<int64_t>(P.chunks, nq) <= cus && P.s8_units <= 2 * 256 && d <= 512 && k <= 256;
+  }
   const int64_t nqq = std::max<int64_t>(nq, 1);
   const int64_t lists = nqq * P.nlists;
   int64_t off = 0;
@@ -936,6 +950,8 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   off = align_up(off + lists * 4, 256);
   P.off_tau = off;
   off = align_up(off + nqq * 4, 256);
+  P.off_tauw = off;
+  if (P.tau_in_scan) off = align_up(off + nqq * 8, 256);
   P.off_umax = off;
   if (P.s8) {
     off = align_up(off + nqq * P.s8_units * 4, 256);
@@ -993,6 +1009,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   int* li = reinterpret_cast<int*>(ws + P.off_li);
   int* cnt = reinterpret_cast<int*>(ws + P.off_cnt);
   float* tau = reinterpret_cast<float*>(ws + P.off_tau);
+  unsigned long long* tauw = reinterpret_cast<unsigned long long*>(ws + P.off_tauw);
   float* umax = reinterpret_cast<float*>(ws + P.off_umax);
   signed char* qq = reinterpret_cast<signed char*>(ws + P.off_qq);
   float4* qm = reinterpret_cast<float4*>(ws + P.off_qm);
@@ -1067,23 +1084,27 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     pa.qmeta = qm;
     pa.bmeta = bmeta;
     pa.gamma = gamma;
+    pa.tauw = P.tau_in_scan ? tauw : nullptr;
+    pa.perm = P.s8_agg ? perm : nullptr;  // units' rows as corpus rows (mapped in the pass's tail)
     e = launch_scan(P.cfg, kMaxQ8, pa, (int)(P.groups * P.s8_nsample), s);
     if (e != hipSuccess) return hip_fail(e, "int8 sample pass launch");
-    SelectArgs ta{};
-    ta.lv = umax;
-    ta.li = pa.uarg;
-    ta.nlists = 1;
-    ta.cap = (int)P.s8_units;
-    ta.k = (int)k;
-    ta.tau = tau;
-    ta.q = qh;
-    ta.x = xh;
-    ta.n = n;
-    ta.d = (int)d;
-    ta.perm = perm;
     mark(1);
-    e = launch_select(5, ta, (int)nq, s);
-    if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+    if (!P.tau_in_scan) {  // (otherwise the int8 scan computes the thresholds itself)
+      SelectArgs ta{};
+      ta.lv = umax;
+      ta.li = pa.uarg;
+      ta.nlists = 1;
+      ta.cap = (int)P.s8_units;
+      ta.k = (int)k;
+      ta.tau = tau;
+      ta.q = qh;
+      ta.x = xh;
+      ta.n = n;
+      ta.d = (int)d;
+      ta.perm = P.s8_agg ? nullptr : perm;
+      e = launch_select(5, ta, (int)nq, s);
+      if (e != hipSuccess) return hip_fail(e, "threshold select launch");
+    }
     mark(2);
   } else if (fp16_sample) {  // exact fp16 sampling pre-pass and threshold, as in cvs_fused_topk
     if (S.gemv) {
@@ -1189,10 +1210,21 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     a.qmeta = qm;
     a.bmeta = bmeta;
     a.gamma = gamma;
-    const ScanCfg c384{32, 8, 1, 2, 12};
-    const bool lean = P.cfg.ms == c384.ms && P.cfg.qs == c384.qs && P.cfg.qb == c384.qb && P.cfg.rb == c384.rb &&
-                      P.cfg.ksmax == c384.ksmax && q8scan384_fits(a);
-    e = lean ? launch_q8scan384(a, (int)(P.groups * P.chunks), s)
+    if (P.tau_in_scan) {
+      a.tau = nullptr;
+      a.tauw = tauw;
+      a.tau_out = tau;
+      a.su_max = umax;
+      a.su_arg = reinterpret_cast<const int*>(ws + P.off_uarg);
+      a.su_units = (int)P.s8_units;
+      a.qh = qh;
+      a.xh = xh;
+      a.dh = (int)d;
+      a.perm = P.s8_agg ? nullptr : perm;
+    }
+    const bool lean = P.lean && q8scan384_fits(a);
+    if (P.tau_in_scan && !lean) return fail(CVS_ERR_INVALID, "internal: in-scan thresholds without the 384-byte int8 scan");
+    e = lean ? launch_q8scan384(a, (int)(P.tau_in_scan ? std::max<int64_t>(P.chunks, nq) : P.groups * P.chunks), s)
              : launch_scan(P.cfg, kAppendQ8, a, (int)(P.groups * P.chunks), s);
     if (e != hipSuccess) return hip_fail(e, "int8 scan launch");
   }

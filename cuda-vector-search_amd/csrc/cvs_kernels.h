@@ -48,7 +48,8 @@ struct ScanArgs {
   int k;
   // kMax
   float* umax;        // [nq, units]
-  int* uarg;          // kMaxQ8: [nq, units] the (companion) row of each unit's maximum
+  int* uarg;          // kMaxQ8: [nq, units] the (companion) row of each unit's maximum; with agg == 1
+                      // and perm (below) not null, its corpus row perm[row]
   int nsample;        // sampling workgroups per query group
   int spt;            // consecutive tiles sampled by each of them
   int agg;            // 1: one unit per (workgroup, row split, lane group) over all its tiles;
@@ -63,6 +64,21 @@ struct ScanArgs {
   const float4* qmeta;  // [nq] (s_q, |q^|_2 up, |e_q|_2 up, 0): query scale and residual norms
   const float4* bmeta;  // [ceil(n/64)] (s_b, max |f_r|_2 up, max |x_r|_2 up, 0) per 64-row block
   float gamma;          // relative slack for fp32 rounding of the scores: (3d + 8) * 2^-24
+  // Thresholds computed inside the int8 scan (cvs_tau_group.h): when tauw is
+  // not null, the kMaxQ8 sampling pass zeroes tauw[0..nq) and the int8 scan
+  // (tau null) takes each query's threshold from the sampling units
+  // su_max / su_arg [nq, su_units] by exact rescoring against the fp16 query
+  // rows qh and corpus xh (dh halfs per row; perm: companion -> corpus row,
+  // null when su_arg holds corpus rows), also stored to tau_out[q].
+  unsigned long long* tauw;
+  float* tau_out;
+  const float* su_max;
+  const int* su_arg;
+  int su_units;
+  const _Float16* qh;
+  const _Float16* xh;
+  int dh;
+  const int* perm;
 };
 
 // Batch-1 GEMV: one query, rows split across waves, 8 lanes per row.

@@ -217,6 +217,11 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     t_end = t_begin + a.tpc < a.ntiles ? t_begin + a.tpc : a.ntiles;
   }
 
+  if constexpr (MODE == kMaxQ8) {  // the words of the thresholds the int8 scan computes: "not yet"
+    if (a.tauw != nullptr && tid == 0)
+      for (int i = blockIdx.x; i < a.nq; i += gridDim.x) a.tauw[i] = 0ull;
+  }
+
   const int d = a.d;
   const int nc = FULLW ? NCMAX : (d >> 6);
   const int64_t n = a.n;
@@ -895,13 +900,19 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   }
   if (APP && st_n > 0) flush();
   if (SMAX && a.agg == 1) {
+    // kMaxQ8 with perm: the units' corpus rows (perm of their companion rows;
+    // the lookups overlap the drain below), so that the threshold needs no
+    // lookup of its own
+    int urow[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) urow[qb] = (MODE == kMaxQ8 && a.perm != nullptr) ? a.perm[uag[qb]] : uag[qb];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
       if (qi < a.nq) {
         const int64_t u = (int64_t)qi * a.units + (chunk * RS + rs) * G + kg;
         a.umax[u] = umx[qb];
-        if (MODE == kMaxQ8) a.uarg[u] = uag[qb];
+        if (MODE == kMaxQ8) a.uarg[u] = urow[qb];
       }
     }
   }

@@ -32,6 +32,7 @@
 
 #include "cvs_common.h"
 #include "cvs_kernels.h"
+#include "cvs_tau_group.h"
 
 namespace cvs {
 
@@ -111,8 +112,45 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     ++it_t;
     it_buf = (it_buf + 1 == kQ8Nbuf) ? 0 : it_buf + 1;
   };
+  static_assert(2 * sizeof(TauGroupShared) <= sizeof(st_ent), "threshold scratch in the staging area");
+  if (a.tauw == nullptr) {
 #pragma unroll
-  for (int i = 0; i < kQ8Nbuf - 1; ++i) issue_next();
+    for (int i = 0; i < kQ8Nbuf - 1; ++i) issue_next();
+  } else {
+    // Thresholds computed here: waves 0-3 take query blockIdx.x (tau_group,
+    // in the staging area, free until the first tile) while waves 4-7 issue
+    // every prologue stage load, their own and those of waves w - 4, so that
+    // no stage load sits in the threshold waves' vmcnt queue ahead of the
+    // threshold's loads.  (Every wave drains its loads before the tile loop.)
+    // The grid may extend past the scan's chunks (one workgroup per query):
+    // those workgroups only compute their query's threshold.
+    const bool tau_only = (int)blockIdx.x >= a.groups * a.nchunks;  // no chunk: thresholds only
+    if (w >= 4 && !tau_only) {
+#pragma unroll
+      for (int i = 0; i < kQ8Nbuf - 1; ++i) {
+        const int64_t tt = t_begin + i < a.ntiles ? t_begin + i : t_last;
+        const unsigned char* base = xq + tt * kQ8Stage;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int ww = w - 4 + 4 * h;
+          const uint32_t lds = lds0 + (uint32_t)(i * kQ8Stage + ww * 1024);
+#pragma unroll
+          for (int j = 0; j < kQ8Lpw; ++j) {
+            const int L = (ww + kQ8Waves * j) * 8 + (lane >> 3);
+            const uint32_t vo = (uint32_t)(L * 128 + (((lane & 7) ^ piece_swz(L / 3)) << 4));
+            dma16_saddr(vo, base, lds + (uint32_t)(j * kQ8Waves * 1024));
+          }
+        }
+      }
+    }
+    it_t = t_begin + (kQ8Nbuf - 1);
+    it_buf = kQ8Nbuf - 1;
+    TauGroupShared* tg = reinterpret_cast<TauGroupShared*>(&st_ent[0][0]);
+    const int qt = (w < 4 && (int)blockIdx.x < a.nq) ? (int)blockIdx.x : -1;
+    tau_group<2, 4, 4>(tg[w >> 2], tid & 255, qt, a.su_max, a.su_arg, a.su_units, a.k, a.qh, a.xh, n, a.dh, a.perm, a.tauw,
+                       a.tau_out);
+    if (tau_only) return;
+  }
 
   // ---- this lane's two queries: fragments (AGPRs), thresholds, bound terms ----
   const unsigned char* qq = reinterpret_cast<const unsigned char*>(a.q);
@@ -134,7 +172,7 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
   for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
     const int qi = grp * kQ8Bq + i;
     lcnt[i] = 0;
-    thr_s[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+    if (a.tauw == nullptr) thr_s[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
   }
   int st_n = 0;  // wave-uniform count of staged entries
 
@@ -244,6 +282,17 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
       acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[ks % 3], qf[1][ks], acc1, 0, 0, 0);
     }
     cur = nxt;
+    if (t == t_begin && a.tauw != nullptr) {
+      // the thresholds computed in the prologue (this workgroup's and the
+      // others'), waited for while the first tile's MFMAs run
+      for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
+        const int qi = grp * kQ8Bq + i;
+        thr_s[i] = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) thr[qb] = thr_s[qgw * 64 + qb * 32 + col];
+    }
     pad_mfma_result<8>(acc1);
     asm volatile("" : "+v"(acc0));
     asm volatile("" : "+v"(acc1));
@@ -302,6 +351,11 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
 }  // namespace
 
 bool q8scan384_fits(const ScanArgs& a) {
+  if (a.tauw != nullptr &&
+      (a.tau != nullptr || a.tau_out == nullptr || a.su_max == nullptr || a.su_arg == nullptr || a.su_units < 1 || a.su_units > 2 * 256 ||
+       a.qh == nullptr || a.xh == nullptr || a.dh < 8 || a.dh % 8 != 0 || a.dh > 8 * 16 * 4 ||
+       a.k < 1 || a.k > 256))
+    return false;
   return a.d * 2 == kQ8Row && a.qmeta != nullptr && a.bmeta != nullptr && a.nlists == a.nchunks;
 }
 

@@ -49,6 +49,7 @@ extern "C" {
 #define CVS_FLAG_FORCE_PREPASS 2 /* run the pre-pass whenever it is well defined */
 #define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
 #define CVS_FLAG_IDS_INT64 8     /* out_i is int64 (the dtype Index.search returns, index.py:126) */
+#define CVS_FLAG_TAU_LAUNCH 16   /* int8 pre-filter: thresholds in a launch of their own, not in the scan */
 
 /* Library version (CVS_VERSION). */
 int cvs_version(void);

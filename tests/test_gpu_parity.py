@@ -929,6 +929,36 @@ def test_q8_forced_sampling_with_few_units(eng, nq, n, d, k):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nq,n,k,forced", [(256, 300000, 10, False), (200, 150000, 10, False), (150, 200000, 32, False),
+                                           (256, 120000, 100, False), (300, 200000, 10, False), (256, 9000, 250, True),
+                                           (137, 5000, 40, True)])
+def test_q8_thresholds_in_the_scan_match_the_threshold_launch(eng, nq, n, k, forced):
+    """The 384-byte int8 scan computes each query's threshold in its prologue
+    (one query per 4 waves of a workgroup, published to the others through
+    64-bit words): bitwise the same results as the separate threshold launch
+    (FLAG_TAU_LAUNCH), and the fused path's.  Covers one and two query groups,
+    the batches whose candidates are rescored by a kernel of their own (fewer
+    than 160 queries: it reads the thresholds the scan stored), and forced
+    sampling over corpora with fewer sampled rows than k (threshold -inf)."""
+    say(f"q8 thresholds in the scan nq={nq} n={n} k={k} forced={forced}")
+    x, q = make(n, 384, nq, seed=n + nq + k)
+    qd = q.cuda().contiguous()
+    xd = x.cuda().contiguous()
+    xq = eng.q8_build(xd)
+    f = _ext.FLAG_FORCE_PREPASS if forced else 0
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k, flags=f)
+    vl, il, _ = eng.q8_topk(qd, xd, xq, k, flags=f | _ext.FLAG_TAU_LAUNCH)
+    v, i, _ = eng.fused_topk(qd, xd, k)
+    torch.cuda.synchronize()
+    assert torch.equal(v8, vl) and torch.equal(i8, il)
+    np.testing.assert_allclose(v8.cpu().numpy(), v.cpu().numpy(), rtol=0, atol=2e-6)
+    same = (i8 == i).cpu().numpy()
+    assert same.all() or np.abs((v8 - v).cpu().numpy())[~same].max() < 2e-6
+    sub = slice(0, 16)  # (the CPU oracle on 16 queries; the rest are pinned to the fused path above)
+    oracle.check_exact(q[sub].numpy(), x.numpy(), k, v8[sub].cpu().numpy(), i8[sub].cpu().numpy().astype(np.int64))
+
+
+@pytest.mark.gpu
 def test_q8_zero_queries_and_rows(eng):
     """All-zero queries (scale 0) and all-zero corpus blocks: every score is 0 and
     ties order by id."""
