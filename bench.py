@@ -41,6 +41,9 @@ first ~100 calls, a hipBLASLt 4096^3 fp16 GEMM 147 -> 121 us the same way, a
 384 MB device copy flat at 153-156 us).  Before its W warm-up steps each config
 therefore runs its step untimed for --settle-ms (default 30) of wall time
 (``settle_calls`` in its row); the timed region is still exactly K steps.
+Beside the settled figure each row carries ``cold_ms_per_batch``: the mean of
+the first 20 back-to-back searches after 2 s of idle, with no settling (the
+ramp a process that searches a few times after idling sees).
 """
 
 from __future__ import annotations
@@ -98,7 +101,7 @@ def end_to_end(n, d, b, k, ms, int8, dq):
     return out
 
 
-def run_config(name, steps, warmup, eng, torch, synthetic, Index, settle_ms=30.0):
+def run_config(name, steps, warmup, eng, torch, synthetic, Index, settle_ms=30.0, cold_idle_s=2.0, cold_calls=20):
     from cuda_vector_search.index import q8_row_bytes
 
     n, d, b, k, ties = synthetic.CONFIGS[name]
@@ -112,6 +115,20 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index, settle_ms=30.0
 
     def step():
         return index.search(q, k)
+
+    # Cold calls: one untimed call (first-use allocations), cold_idle_s of idle,
+    # then the first cold_calls searches back to back, each event-timed: the
+    # unsettled clocks a process sees after idling (module docstring).
+    step()
+    torch.cuda.synchronize()
+    time.sleep(cold_idle_s)
+    cold_ev = [torch.cuda.Event(enable_timing=True) for _ in range(cold_calls + 1)]
+    cold_ev[0].record()
+    for i in range(cold_calls):
+        step()
+        cold_ev[i + 1].record()
+    torch.cuda.synchronize()
+    cold_ms = [cold_ev[i].elapsed_time(cold_ev[i + 1]) for i in range(cold_calls)]
 
     settle_calls = 0  # untimed, until the clocks have settled (module docstring)
     t_settle = time.perf_counter() + settle_ms / 1000.0
@@ -180,6 +197,9 @@ def run_config(name, steps, warmup, eng, torch, synthetic, Index, settle_ms=30.0
         "config": name, "n": n, "d": d, "batch": b, "k": k, "near_ties": ties,
         "plan": [int(v) for v in plan.tolist()],
         "settle_calls": settle_calls,
+        "cold_ms_per_batch": round(statistics.fmean(cold_ms), 4),
+        "cold_first_last_ms": [round(cold_ms[0], 4), round(cold_ms[-1], 4)],
+        "cold_sample": f"{cold_calls} back-to-back calls after {cold_idle_s:g} s idle, no settling; event-timed",
         "ms_per_batch": round(wall_ms, 4), "device_ms_per_batch": round(dev_ms, 4),
         "qps": round(b / (wall_ms / 1000.0), 1),
         "path": "int8" if int8 else "fused",

@@ -174,6 +174,7 @@ struct Plan {
   // sampling pre-pass
   bool prepass = false;
   bool tau_in_scan = false;  // one sampling maximum per workgroup, thresholds found by the scan
+  bool topk = false;         // CVS_FLAG_REGISTER_TOPK: running top-k in registers, no pre-pass
   int64_t nsample = 0, spt = 1, units = 0;
   int agg = 0;
   int upb = 8;  // gemv sampling units per block
@@ -220,6 +221,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
   } else {
     if (!forced_bq) {
       bq = nq <= 16 ? 16 : nq <= 32 ? 32 : nq <= 64 ? 64 : (nq <= 128 || d != 384) ? 128 : 256;
+      if ((flags & CVS_FLAG_REGISTER_TOPK) && nq <= 32) bq = 32;  // (the register top-k's 32-query block)
       ScanCfg tmp;
       while (!cfg_for(bq, d, &tmp)) bq >>= 1;
     }
@@ -286,6 +288,13 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
         P.units = P.nsample;
       }
     }
+  }
+  if (flags & CVS_FLAG_REGISTER_TOPK) {
+    if (P.gemv || !scan_topk_available(P.cfg, d, k))
+      return fail(CVS_ERR_INVALID, "the register top-k scan covers batches of 2..32 at widths <= 384 and k <= 16");
+    P.topk = true;
+    P.prepass = false;
+    P.tau_in_scan = false;
   }
   if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
   const int64_t lists = std::max<int64_t>(nq, 1) * P.nlists;
@@ -474,7 +483,8 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
     a.li = li;
     a.lcount = cnt;
     a.nlists = (int)P.nlists;
-    e = launch_scan(P.cfg, kAppend, a, (int)(P.groups * P.chunks), s);
+    e = P.topk ? launch_scan_topk(P.cfg, a, (int)(P.groups * P.chunks), s)
+               : launch_scan(P.cfg, kAppend, a, (int)(P.groups * P.chunks), s);
     if (e != hipSuccess) return hip_fail(e, "scan launch");
     mark(3);
   }

@@ -16,6 +16,8 @@ enum ScanMode : int {
                   // upper bound reaches the threshold (no compaction; full lists overflow)
   kMaxQ8 = 5,     // int8 sample pass: per-(query, unit) largest approximate score
                   // A = s_q s_b sum(q~ x~) over disjoint row sets, and its row
+  kTopK = 6,      // no threshold: each lane keeps the k <= 16 best of its own scores of
+                  // each query in registers (a running top-k) and appends them at the end
 };
 
 // One tile of corpus rows is scored against a group of queries by one
@@ -214,6 +216,9 @@ struct ScanCfg {
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for (cfg, mode).
 hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid, hipStream_t s);
+// Mode kTopK: instantiated for cfg {32, 1, 1, 1, 24} only (batches <= 32, width <= 384).
+bool scan_topk_available(const ScanCfg& cfg, int64_t d, int64_t k);
+hipError_t launch_scan_topk(const ScanCfg& cfg, const ScanArgs& a, int grid, hipStream_t s);
 // int8 scan of 384-byte rows at 256 queries per workgroup (cfg {32, 8, 1, 2, 12}):
 // the same lists as launch_scan(cfg, kAppendQ8, ...), from a leaner kernel.
 bool q8scan384_fits(const ScanArgs& a);

@@ -159,7 +159,9 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr bool PAIR = FULLW && (NCMAX % 2 == 0) && NBUF >= 5;
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
+  constexpr bool TOPK = (MODE == kTopK);
   constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8);
+  static_assert(!TOPK || (QB == 1 && MS == 32), "running top-k: one 32-query block per wave");
   constexpr bool SMAX = (MODE == kMax || MODE == kMaxQ8);  // sample passes
   constexpr int STCAP = 64;          // staged entries per wave
   // A staged entry is one lane's NE scores of one (query block, row block): a
@@ -171,6 +173,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NBUF * STAGE];
   __shared__ int lcnt[RS][BQ];                        // entries in each owned list
+  __shared__ uint32_t thr_k[TOPK ? BQ : 1];           // kTopK: the workgroup's per-query k-th best so far (order key)
   __shared__ float thr_s[APP ? RS : 1][BQ];           // per-query filter threshold
   __shared__ float mred[MODE == kMax ? RS : 1][BQ];    // kMax, agg 2: maxima of the row splits
   __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
@@ -362,12 +365,32 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       for (int j = 0; j < 8; ++j) kraw[j] = src[min((tid & 7) + 8 * j, a.units_in - 1)];
     }
   }
-  if (APP) {
+  if (APP || TOPK) {
     for (int i = tid; i < RS * BQ; i += NT) {
       (&lcnt[0][0])[i] = 0;
       const int qi = grp * BQ + i % BQ;
       if (!thr_in) (&thr_s[0][0])[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
     }
+  }
+  // kTopK: this lane's running top-k of each query block in the last k of
+  // TK slots, descending (the first TK - k slots are parked at +inf, so the
+  // k-th best is always the last slot; real slots not yet filled hold -inf
+  // and row -1), and the workgroup's threshold: the largest k-th best of any
+  // lane holding the query, a lower bound of the workgroup's own k-th best
+  // (that lane has k scores at or above it).
+  constexpr int TK = TOPK ? 16 : 1;
+  float tkv[QB][TK];
+  int tki[QB][TK];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+      tkv[qb][j] = j < TK - a.k ? __builtin_inff() : -__builtin_inff();
+      tki[qb][j] = -1;
+    }
+  if constexpr (TOPK) {
+    for (int i = tid; i < RS * BQ; i += NT) (&lcnt[0][0])[i] = 0;
+    for (int i = tid; i < BQ; i += NT) thr_k[i] = float_order(-__builtin_inff());
   }
   int st_n = 0;  // wave-uniform count of staged lane-rows
   float umx[QB];  // kMax / kMaxQ8 with agg: this lane's unit maxima over all sampled tiles
@@ -839,6 +862,33 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
               *(half4*)((_Float16*)stg[w] + qo + r) =
                   half4{(_Float16)v[j], (_Float16)v[j + 1], (_Float16)v[j + 2], (_Float16)v[j + 3]};
           }
+        } else if constexpr (TOPK) {
+          // Each of the lane's scores above its own k-th best and not below the
+          // workgroup's threshold enters its list (a med3 insertion network; equal
+          // scores keep the earlier, smaller row first).  Rows arrive in
+          // ascending order per lane.  A score position no lane inserts is skipped.
+          const float tw = order_float(thr_k[qs * QW + qb * MS + col]);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int e = 0; e < M::NE; ++e) {
+              const float sc = v[rb * M::NE + e];
+              const bool ins = sc > tkv[qb][TK - 1] && sc >= tw && qi < a.nq;
+              if (__ballot(ins)) {
+                if (ins) {
+                  const int r = (int)rowb + rb * MS + M::row(e);
+#pragma unroll
+                  for (int j = TK - 1; j >= 1; --j) {
+                    const bool up = sc > tkv[qb][j - 1], here = sc > tkv[qb][j];
+                    tki[qb][j] = up ? tki[qb][j - 1] : (here ? r : tki[qb][j]);
+                    tkv[qb][j] = __builtin_amdgcn_fmed3f(tkv[qb][j - 1], tkv[qb][j], sc);
+                  }
+                  tki[qb][0] = sc > tkv[qb][0] ? r : tki[qb][0];
+                  tkv[qb][0] = fmaxf(tkv[qb][0], sc);
+                }
+              }
+            }
+          if (qi < a.nq) atomicMax(&thr_k[qs * QW + qb * MS + col], float_order(tkv[qb][TK - 1]));
         } else if (MODE == kMax) {
           float m = v[0];
 #pragma unroll
@@ -899,6 +949,36 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     }
   }
   if (APP && st_n > 0) flush();
+  if constexpr (TOPK) {
+    // every lane's entries not below the workgroup's final threshold (real
+    // rows only) into its wave's list of the query
+    __syncthreads();
+    const int list = chunk * RS + rs;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int ql = qs * QW + qb * MS + col;
+      const int qi = grp * BQ + ql;
+      const float tw = order_float(thr_k[ql]);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < TK; ++j) c += (tki[qb][j] >= 0 && tkv[qb][j] >= tw) ? 1 : 0;
+      if (qi < a.nq && c > 0) {
+        const int pos = atomicAdd(&lcnt[rs][ql], c);
+        const int64_t lbase = ((int64_t)qi * a.nlists + list) * a.cap;
+        int put = 0;
+#pragma unroll
+        for (int j = 0; j < TK; ++j) {
+          if (tki[qb][j] >= 0 && tkv[qb][j] >= tw) {
+            if (pos + put < a.cap) {
+              a.lv[lbase + pos + put] = tkv[qb][j];
+              a.li[lbase + pos + put] = tki[qb][j];
+            }
+            ++put;
+          }
+        }
+      }
+    }
+  }
   if (SMAX && a.agg == 1) {
     // kMaxQ8 with perm: the units' corpus rows (perm of their companion rows;
     // the lookups overlap the drain below), so that the threshold needs no
@@ -940,7 +1020,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       }
     }
   }
-  if (APP) {
+  if (APP || TOPK) {
     for (int i = tid; i < RS * BQ; i += NT) {
       const int r = i / BQ;
       const int ql = i % BQ;
@@ -1038,6 +1118,16 @@ hipError_t launch_one(int mode, const ScanArgs& a, int grid, hipStream_t s) {
   X(32, 8, 1, 2, 24)
 
 }  // namespace
+
+bool scan_topk_available(const ScanCfg& c, int64_t d, int64_t k) {
+  return c.ms == 32 && c.qs == 1 && c.qb == 1 && c.rb == 1 && c.ksmax == 24 && d <= 384 && k >= 1 && k <= 16;
+}
+
+hipError_t launch_scan_topk(const ScanCfg& c, const ScanArgs& a, int grid, hipStream_t s) {
+  if (!scan_topk_available(c, a.d, a.k) || a.cap < 2 * 16 || a.nlists != a.nchunks * c.rs()) return hipErrorInvalidValue;
+  launch_mode<32, 1, 1, 1, 24, kTopK>(a.d == 24 * 16, a, grid, s);
+  return hipGetLastError();
+}
 
 bool scan_cfg_available(const ScanCfg& c, int mode) {
   if (mode == kAppendQ8 || mode == kMaxQ8) {

@@ -50,6 +50,8 @@ extern "C" {
 #define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
 #define CVS_FLAG_IDS_INT64 8     /* out_i is int64 (the dtype Index.search returns, index.py:126) */
 #define CVS_FLAG_TAU_LAUNCH 16   /* int8 pre-filter: thresholds in a launch of their own, not in the scan */
+#define CVS_FLAG_REGISTER_TOPK 32 /* fp16 fused path: a running top-k per lane in registers instead of the
+                                     sampled threshold (batches 2..32, widths <= 384, k <= 16) */
 
 /* Library version (CVS_VERSION). */
 int cvs_version(void);

@@ -298,6 +298,35 @@ def test_forced_prepass_with_fewer_finite_units_than_k(eng, n, d, b, k):
     assert same.all() or np.abs(v8 - v)[~same].max() < 2e-6
 
 
+@pytest.mark.parametrize("n,d,b,k", [(100000, 384, 32, 10), (20000, 384, 13, 16), (5000, 256, 2, 1),
+                                     (3000, 128, 32, 16), (129, 384, 20, 16), (60000, 320, 32, 7)])
+def test_register_topk_scan_matches_the_sampled_threshold(eng, n, d, b, k):
+    """The running top-k in registers (FLAG_REGISTER_TOPK: no sampling pass,
+    each lane's k best kept in VGPRs, the workgroup's k-th best shared through
+    LDS): the oracle's results, bitwise those of the default path."""
+    say(f"register top-k n={n} d={d} b={b} k={k}")
+    x, q = make(n, d, b, seed=n + b + k)
+    v, i, _ = run_fused(eng, q, x, k, flags=_ext.FLAG_REGISTER_TOPK)
+    oracle.check_exact(q, x, k, v, i)
+    v0, i0, _ = run_fused(eng, q, x, k)
+    np.testing.assert_array_equal(v, v0)
+    np.testing.assert_array_equal(i, i0)
+
+
+def test_register_topk_scan_with_exact_duplicates(eng):
+    """Bit-identical rows across lanes and workgroups: ties come out in id order."""
+    say("register top-k, duplicates")
+    x, q = make(30000, 384, 24, seed=77)
+    src = torch.arange(0, 30000, 97)
+    x[src + 1] = x[src]  # pairs of equal rows
+    x[src[:50] + 2] = x[src[:50]]
+    v, i, _ = run_fused(eng, q, x, 16, flags=_ext.FLAG_REGISTER_TOPK)
+    v0, i0, _ = run_fused(eng, q, x, 16)
+    np.testing.assert_array_equal(v, v0)
+    np.testing.assert_array_equal(i, i0)
+    oracle.check_exact(q, x, 16, v, i)
+
+
 @pytest.mark.parametrize("k", [10, 100])
 def test_two_group_sampling_on_paired_xcds(eng, k):
     """d = 768 at b = 256 runs two 128-query groups; with 128 sampling
