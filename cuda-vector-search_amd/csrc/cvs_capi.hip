@@ -855,7 +855,7 @@ struct Q8Plan {
   // the thresholds itself (tau_in_scan) instead of a threshold launch
   bool lean = false, tau_in_scan = false;
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_tauw = 0, off_umax = 0, off_uarg = 0, off_qq = 0,
-          off_qm = 0, ws_bytes = 0;
+          off_qm = 0, off_qf = 0, ws_bytes = 0;
 };
 
 int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus, Q8Plan* out) {
@@ -974,6 +974,8 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   off = align_up(off + nqq * P.dq, 256);
   P.off_qm = off;
   off = align_up(off + nqq * 16, 256);
+  P.off_qf = off;  // the int8 queries again, in the scans' fragment order (whole 32-query blocks)
+  off = align_up(off + align_up(nqq, 32) * P.dq, 256);
   P.ws_bytes = off;
   *out = P;
   return CVS_OK;
@@ -1023,6 +1025,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   float* umax = reinterpret_cast<float*>(ws + P.off_umax);
   signed char* qq = reinterpret_cast<signed char*>(ws + P.off_qq);
   float4* qm = reinterpret_cast<float4*>(ws + P.off_qm);
+  signed char* qf = reinterpret_cast<signed char*>(ws + P.off_qf);
   const _Float16* qh = static_cast<const _Float16*>(q);
   const _Float16* xh = static_cast<const _Float16*>(x);
   const Plan& S = P.sample;
@@ -1033,7 +1036,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   hipError_t e;
 
   if (!fp16_sample) {  // otherwise the threshold select quantises the queries on the way
-    Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm};
+    Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm, qf};
     e = launch_q8_queries(qa, s);
     if (e != hipSuccess) return hip_fail(e, "query quantisation launch");
   }
@@ -1074,6 +1077,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   } else if (P.s8) {  // int8 sampling pass; the threshold from rescoring its best units' rows
     ScanArgs pa{};
     pa.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
+    pa.qf = qf;
     pa.x = static_cast<const _Float16*>(xq);
     pa.n = n;
     pa.nq = (int)nq;
@@ -1153,6 +1157,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       pa.xcd_pair = (S.groups > 1 && S.nsample % 8 == 0) ? 1 : 0;
       pa.units = (int)S.units;
       pa.qq_out = qq;  // the sampling scan quantises the queries on the way
+      pa.qf_out = qf;
       pa.qmeta_out = qm;
       pa.dq = (int)P.dq;
       e = launch_scan(S.cfg, kMax, pa, (int)(S.groups * S.nsample), s);
@@ -1167,6 +1172,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     sa.q = qh;
     sa.d = (int)d;
     sa.qq_out = S.gemv ? qq : nullptr;  // (after a GEMV sampling pass the threshold select quantises)
+    sa.qf_out = S.gemv ? qf : nullptr;
     sa.qmeta_out = qm;
     sa.dq = (int)P.dq;
     mark(1);
@@ -1201,6 +1207,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   } else {
     ScanArgs a{};
     a.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
+    a.qf = qf;
     a.x = static_cast<const _Float16*>(xq);
     a.n = n;
     a.nq = (int)nq;

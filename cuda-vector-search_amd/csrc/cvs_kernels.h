@@ -58,12 +58,14 @@ struct ScanArgs {
                       // 2: one unit per workgroup (units = nsample)
   int units;          // units per query = nsample * (agg ? 1 : spt) * units_per_tile
   signed char* qq_out;  // kMax: when not null, also quantise the queries for the int8 pre-filter:
-  float4* qmeta_out;    //   qq_out[nq, dq] int8 rows and qmeta_out[nq] (see cvs_q8_row.h)
+  float4* qmeta_out;    //   qq_out[nq, dq] int8 rows and qmeta_out[nq] (see cvs_q8_row.h),
+  signed char* qf_out;  //   and the same bytes in fragment order into qf_out (q8_frag_offset)
   int dq;
   // kStore*
   void* out;          // [nq, n]
   // kAppendQ8 (q, x are int8 rows viewed as 2-byte units: d = row bytes / 2)
   const float4* qmeta;  // [nq] (s_q, |q^|_2 up, |e_q|_2 up, 0): query scale and residual norms
+  const signed char* qf;  // the int8 queries in fragment order (q8_frag_offset): what the MFMAs load
   const float4* bmeta;  // [ceil(n/64)] (s_b, max |f_r|_2 up, max |x_r|_2 up, 0) per 64-row block
   float gamma;          // relative slack for fp32 rounding of the scores: (3d + 8) * 2^-24
   // Thresholds computed inside the int8 scan (cvs_tau_group.h): when tauw is
@@ -164,9 +166,11 @@ struct SelectArgs {
   const float* xmax;      // max |x_r|_2 over the corpus (rounded up)
   float gamma;            // d * 2^-24 (one rounding per accumulated term)
   // threshold mode, int8 pre-filter: also quantise query row q (q, d above)
-  // into qq_out[q * dq ..] and qmeta_out[q] (when qq_out is not null)
+  // into qq_out[q * dq ..] and qmeta_out[q] (when qq_out is not null), and
+  // in fragment order into qf_out (q8_frag_offset; when qf_out is not null)
   signed char* qq_out;
   float4* qmeta_out;
+  signed char* qf_out;
   int dq;
   // rescore mode: list entries and list ranges are rows of the int8 companion,
   // whose row r is corpus row perm[r] (null: the identity)
@@ -194,6 +198,7 @@ struct Q8QueryArgs {
   int dq;
   signed char* qq;     // [nq, dq]
   float4* qmeta;       // [nq]
+  signed char* qf;     // when not null: the same bytes in fragment order (q8_frag_offset), 32 * ceil(nq / 32) * dq bytes
 };
 
 // Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void q8_xmax_kernel(const float4* bmeta, in
 __global__ __launch_bounds__(kBlock) void q8_query_kernel(Q8QueryArgs a) {
   const int64_t r = (int64_t)blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
   if (r >= a.nq) return;  // whole wave
-  q8_query_row(a.q + r * a.d, a.d, a.dq, a.qq + r * a.dq, a.qmeta + r, threadIdx.x & 63);
+  q8_query_row(a.q + r * a.d, a.d, a.dq, a.qq + r * a.dq, a.qmeta + r, threadIdx.x & 63, a.qf, r);
 }
 
 }  // namespace

@@ -30,10 +30,22 @@ __device__ __forceinline__ void q8_load_row(const _Float16* src, int d, int lane
   }
 }
 
+// Fragment order of the int8 queries, the B operand of the 32x32x32 int8
+// MFMA as the scans hold it: bytes [32 ks + 16 kg, +16) of query qi sit at
+// this offset, KS = dq / 32 k-steps per row.  A wave's fragments of one
+// k-step for 32 consecutive queries (lane = column + 32 kg) are then 1 KiB of
+// contiguous memory, where the row layout spreads them over 32 rows.
+__device__ __forceinline__ int64_t q8_frag_offset(int64_t qi, int ks, int kg, int KS) {
+  return (((qi >> 5) * KS + ks) * 64 + (qi & 31) + 32 * kg) * 16;
+}
+
 // Whole wave, on the values q8_load_row loaded; `lane` = lane id.  dst holds
-// dq >= d bytes (zero past d; dq % 8 == 0), written 8 bytes per lane.
+// dq >= d bytes (zero past d; dq % 32 == 0), written 8 bytes per lane; when
+// frag is not null the same bytes also go to query qi's places in the
+// fragment-ordered copy frag (q8_frag_offset).
 __device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int d, int dq, signed char* dst,
-                                                float4* meta, int lane) {
+                                                float4* meta, int lane, signed char* frag = nullptr,
+                                                int64_t qi = 0) {
   constexpr float kNormUp = 1.0f + 1.0f / 2048.0f;
   float m = 0.f;
 #pragma unroll
@@ -56,7 +68,10 @@ __device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int
       ee = fmaf(e, e, ee);
       packed |= (uint64_t)(uint8_t)qc << (8 * j);
     }
-    if (c < dq) *(uint64_t*)(dst + c) = packed;
+    if (c < dq) {
+      *(uint64_t*)(dst + c) = packed;
+      if (frag != nullptr) *(uint64_t*)(frag + q8_frag_offset(qi, c >> 5, (c >> 4) & 1, dq >> 5) + (c & 15)) = packed;
+    }
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -74,10 +89,10 @@ __device__ __forceinline__ void q8_quantize_row(const float (&v)[kQ8RowPer], int
 }
 
 __device__ __forceinline__ void q8_query_row(const _Float16* src, int d, int dq, signed char* dst, float4* meta,
-                                             int lane) {
+                                             int lane, signed char* frag, int64_t qi) {
   float v[kQ8RowPer];
   q8_load_row(src, d, lane, v);
-  q8_quantize_row(v, d, dq, dst, meta, lane);
+  q8_quantize_row(v, d, dq, dst, meta, lane, frag, qi);
 }
 
 }  // namespace cvs

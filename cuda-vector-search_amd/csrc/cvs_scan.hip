@@ -327,8 +327,12 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = min(qwave0 + qb * MS + col, a.nq - 1);
 #pragma unroll
-      for (int ks = 0; ks < KSMAX; ++ks)
-        ld[qb][ks] = *(const half8*)(a.q + (int64_t)qi * d + min(ks, ksl) * M::KSZ + kg * 8);
+      for (int ks = 0; ks < KSMAX; ++ks) {
+        if constexpr (Q8)  // full-width int8 rows (KSMAX k-steps): the fragment-ordered copy, 1 KiB per load
+          ld[qb][ks] = *(const half8*)(a.qf + q8_frag_offset(qi, ks, kg, KSMAX));
+        else
+          ld[qb][ks] = *(const half8*)(a.q + (int64_t)qi * d + min(ks, ksl) * M::KSZ + kg * 8);
+      }
     }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -489,7 +493,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       for (int qi = blockIdx.x + w * gridDim.x; qi < a.nq; qi += NW * gridDim.x) {
         float v[kQ8RowPer];
         q8_load_row(a.q + (int64_t)qi * d, d, lane, v);
-        q8_quantize_row(v, d, a.dq, a.qq_out + (int64_t)qi * a.dq, a.qmeta_out + qi, lane);
+        q8_quantize_row(v, d, a.dq, a.qq_out + (int64_t)qi * a.dq, a.qmeta_out + qi, lane, a.qf_out, qi);
       }
     }
   }
@@ -1033,7 +1037,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 // int8 pre-filter: full-width rows only (the int8 row bytes are padded to 32 * KS).
 template <int MS, int QS, int QB, int RB, int KS>
 hipError_t launch_one_q8(int mode, const ScanArgs& a, int grid, hipStream_t s) {
-  if (a.d != KS * MfmaI8::KSZ || a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
+  if (a.d != KS * MfmaI8::KSZ || a.qf == nullptr || a.qmeta == nullptr || a.bmeta == nullptr) return hipErrorInvalidValue;
   if (mode == kMaxQ8) {
     if (a.umax == nullptr || a.uarg == nullptr || a.nsample < 1 || a.spt < 1 || a.agg < 0 || a.agg > 1)
       return hipErrorInvalidValue;

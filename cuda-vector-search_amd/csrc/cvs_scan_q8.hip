@@ -19,7 +19,7 @@
 //    64-row blocks, so no DMA load needs a bounds clamp: each of a wave's 3
 //    loads per stage is global_load_lds_dwordx4 from a scalar 64-bit tile base
 //    plus a constant 32-bit lane offset (no per-load vector address
-//    arithmetic), and prefetches past the corpus re-read its last tile.
+//    arithmetic); stages past the workgroup's own tiles are not loaded.
 //  * The tile's block meta comes through the scalar cache, loaded one tile
 //    ahead and consumed after the next top-of-tile wait.
 //
@@ -32,6 +32,7 @@
 
 #include "cvs_common.h"
 #include "cvs_kernels.h"
+#include "cvs_q8_row.h"
 #include "cvs_tau_group.h"
 
 namespace cvs {
@@ -103,14 +104,36 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
   }
   int64_t it_t = t_begin;
   int it_buf = 0;
+  // Stages past this workgroup's tiles are not loaded (the tile loop's waits
+  // account for it): prefetching them would read another chunk's tiles, ~5%
+  // of the corpus again over a launch, and the final drain would wait for them.
   auto issue_next = [&]() {
-    const int64_t tt = it_t < a.ntiles ? it_t : t_last;
-    const unsigned char* base = xq + tt * kQ8Stage;
-    const uint32_t lds = lds0 + (uint32_t)(it_buf * kQ8Stage + w * 1024);
+    if (it_t < t_end) {
+      const unsigned char* base = xq + it_t * kQ8Stage;
+      const uint32_t lds = lds0 + (uint32_t)(it_buf * kQ8Stage + w * 1024);
 #pragma unroll
-    for (int j = 0; j < kQ8Lpw; ++j) dma16_saddr(voff[j], base, lds + (uint32_t)(j * kQ8Waves * 1024));
+      for (int j = 0; j < kQ8Lpw; ++j) dma16_saddr(voff[j], base, lds + (uint32_t)(j * kQ8Waves * 1024));
+    }
     ++it_t;
     it_buf = (it_buf + 1 == kQ8Nbuf) ? 0 : it_buf + 1;
+  };
+  // ---- this lane's two queries: fragments (AGPRs), thresholds, bound terms ----
+  i32x4 qf[2][kQ8Ks];
+  float thr[2];
+  float4 qm[2];
+  auto load_queries = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qi = grp * kQ8Bq + qgw * 64 + qb * 32 + col;
+      const int qc = min(qi, a.nq - 1);  // columns past nq load the last query; their threshold is +inf
+      i32x4 ld[kQ8Ks];
+#pragma unroll
+      for (int ks = 0; ks < kQ8Ks; ++ks) ld[ks] = *(const i32x4*)(a.qf + q8_frag_offset(qc, ks, kg, kQ8Ks));
+#pragma unroll
+      for (int ks = 0; ks < kQ8Ks; ++ks) qf[qb][ks] = pin_agpr(ld[ks]);
+      thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+      qm[qb] = a.qmeta[qc];
+    }
   };
   static_assert(2 * sizeof(TauGroupShared) <= sizeof(st_ent), "threshold scratch in the staging area");
   if (a.tauw == nullptr) {
@@ -128,8 +151,8 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     if (w >= 4 && !tau_only) {
 #pragma unroll
       for (int i = 0; i < kQ8Nbuf - 1; ++i) {
-        const int64_t tt = t_begin + i < a.ntiles ? t_begin + i : t_last;
-        const unsigned char* base = xq + tt * kQ8Stage;
+        if (t_begin + i >= t_end) break;  // (as issue_next: only this workgroup's tiles)
+        const unsigned char* base = xq + (t_begin + i) * kQ8Stage;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int ww = w - 4 + 4 * h;
@@ -151,24 +174,11 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
                        a.tau_out);
     if (tau_only) return;
   }
+  // (After the thresholds: issued before them, by any of the waves, these
+  // loads queue ahead of the threshold's in the CU's memory pipeline and
+  // delay it by more than they gain.)
+  load_queries();
 
-  // ---- this lane's two queries: fragments (AGPRs), thresholds, bound terms ----
-  const unsigned char* qq = reinterpret_cast<const unsigned char*>(a.q);
-  i32x4 qf[2][kQ8Ks];
-  float thr[2];
-  float4 qm[2];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = grp * kQ8Bq + qgw * 64 + qb * 32 + col;
-    const int qc = min(qi, a.nq - 1);  // columns past nq load the last query; their threshold is +inf
-    i32x4 ld[kQ8Ks];
-#pragma unroll
-    for (int ks = 0; ks < kQ8Ks; ++ks) ld[ks] = *(const i32x4*)(qq + (int64_t)qc * kQ8Row + ks * 32 + kg * 16);
-#pragma unroll
-    for (int ks = 0; ks < kQ8Ks; ++ks) qf[qb][ks] = pin_agpr(ld[ks]);
-    thr[qb] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
-    qm[qb] = a.qmeta[qc];
-  }
   for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
     const int qi = grp * kQ8Bq + i;
     lcnt[i] = 0;
@@ -254,11 +264,6 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
 
 #pragma unroll 1
   for (int64_t t = t_begin; t < t_end; ++t) {
-    // Stage t+1 has landed for every wave, and every read of the buffer that
-    // issue_next() refills (stage t-1's) has retired.
-    wait_vmcnt_lgkm0<(kQ8Nbuf - 3) * kQ8Lpw>();
-    __builtin_amdgcn_s_barrier();
-    issue_next();
     const float4 bm = bm_next;
     {
       const int64_t tn = t + 1 < t_last ? t + 1 : t_last;
@@ -274,6 +279,24 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     }
 #pragma unroll
     for (int ks = 0; ks < kQ8Ks; ++ks) {
+      if (ks == kQ8Ks - 2) {
+        // The fragments read from here on are stage t+1's (the current
+        // stage's were published by the previous tile's barrier, so the
+        // MFMAs above overlap the waves' arrival here).  Stage t+1 has landed
+        // for every wave, and every read of the buffer that issue_next()
+        // refills (stage t-1's) has retired.  Stage t+2's loads may still be
+        // in flight, when it exists: near the end there is nothing after
+        // stage t+1 to leave outstanding.  (Exact for a ring of 4: one stage,
+        // t+2, may be outstanding, and it exists exactly when t + 2 < t_end.)
+        static_assert(kQ8Nbuf == 4, "the end-of-range wait counts assume a ring of 4 stages");
+        if (t + 2 < t_end)
+          wait_vmcnt_lgkm0<(kQ8Nbuf - 3) * kQ8Lpw>();
+        else
+          wait_vmcnt_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");  // no LDS read moves above the barrier
+        issue_next();
+      }
       if (ks + 2 < kQ8Ks)
         fr[(ks + 2) % 3] = frag(cur, ks + 2);
       else
@@ -356,7 +379,7 @@ bool q8scan384_fits(const ScanArgs& a) {
        a.qh == nullptr || a.xh == nullptr || a.dh < 8 || a.dh % 8 != 0 || a.dh > 8 * 16 * 4 ||
        a.k < 1 || a.k > 256))
     return false;
-  return a.d * 2 == kQ8Row && a.qmeta != nullptr && a.bmeta != nullptr && a.nlists == a.nchunks;
+  return a.d * 2 == kQ8Row && a.qf != nullptr && a.qmeta != nullptr && a.bmeta != nullptr && a.nlists == a.nchunks;
 }
 
 hipError_t launch_q8scan384(const ScanArgs& a, int grid, hipStream_t s) {

@@ -574,7 +574,8 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
 
   const int nb = min(S.nbuf, k);
   if (MODE == kSelTau) {
-    if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave);
+    if (quant)
+      q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, tid - kWave, a.qf_out, q);
     // the k-th best key is the smallest survivor
     if (tid < kWave) {
       uint64_t m = ~0ull;
@@ -630,7 +631,7 @@ __global__ __launch_bounds__(kWave) void tau_kernel(SelectArgs a) {
     }
   }
   if (lane == 0) a.tau[q] = (m >= a.k) ? order_threshold(t) : -__builtin_inff();
-  if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane);
+  if (quant) q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane, a.qf_out, q);
 }
 
 // Threshold mode with up to U * 256 units per query (one list, as tau_kernel
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(kBlock) void tau_block_kernel(SelectArgs a) {
   if (a.qq_out != nullptr && w == 0) {
     float qrow[kQ8RowPer];
     q8_load_row(a.q + (int64_t)q * a.d, a.d, lane, qrow);
-    q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane);
+    q8_quantize_row(qrow, a.d, a.dq, a.qq_out + (int64_t)q * a.dq, a.qmeta_out + q, lane, a.qf_out, q);
   }
 }
 
@@ -1392,7 +1393,7 @@ hipError_t launch_select(int mode, const SelectArgs& a, int nq, hipStream_t s) {
     case kSelTau:
       if (a.qq_out != nullptr &&
           (a.q == nullptr || a.qmeta_out == nullptr || a.d < 8 || a.d % 8 != 0 || a.d > a.dq || a.dq % 8 != 0 ||
-           a.dq > kQ8RowPer * kWave))
+           a.dq > kQ8RowPer * kWave || (a.qf_out != nullptr && a.dq % 32 != 0)))
         return hipErrorInvalidValue;
       if (a.nlists == 1 && a.li == nullptr && a.lcount == nullptr && a.cap >= 1 && a.cap <= 8 * kWave) {
         // one list of at most 512 unit maxima per query: the one-wave kernel
