@@ -849,11 +849,14 @@ struct Q8Plan {
   // int8 sampling pass (scan mode kMaxQ8) over about 1/kQ8SampleDiv of the
   // int8 tiles, instead of the fp16 one (`sample`) for batches
   bool s8 = false;
-  int64_t s8_nsample = 0, s8_spt = 1, s8_units = 0;
+  int64_t s8_tiles = 0, s8_nsample = 0, s8_spt = 1, s8_units = 0;
   int s8_agg = 0;
-  // the lean 384-byte-row int8 scan (q8scan384_kernel), and whether it takes
-  // the thresholds itself (tau_in_scan) instead of a threshold launch
+  // the lean 384-byte-row int8 scan (q8scan384_kernel), and whether it
+  // samples and takes the thresholds itself (tau_in_scan: in_spt tiles per
+  // workgroup, in_units units per query) instead of the sampling pass and
+  // the threshold launch
   bool lean = false, tau_in_scan = false;
+  int64_t in_spt = 0, in_units = 0;
   int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_tauw = 0, off_umax = 0, off_uarg = 0, off_qq = 0,
           off_qm = 0, off_qf = 0, ws_bytes = 0;
 };
@@ -923,6 +926,7 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
     P.s8 = !(flags & CVS_FLAG_NO_PREPASS) &&
            (((flags & CVS_FLAG_FORCE_PREPASS) && s >= 1) || (s >= 4 && s * upt >= 2 * k));
     if (P.s8) {
+      P.s8_tiles = s;
       const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>({s, cus / P.groups, (16 * 256) / upt}));
       P.s8_spt = std::max<int64_t>(1, s / wgs);
       P.s8_nsample = wgs;
@@ -942,12 +946,20 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
     const ScanCfg c384{32, 8, 1, 2, 12};
     P.lean = P.cfg.ms == c384.ms && P.cfg.qs == c384.qs && P.cfg.qb == c384.qb && P.cfg.rb == c384.rb &&
              P.cfg.ksmax == c384.ksmax && P.dq == 384 && P.nlists == P.chunks;
-    // In-scan thresholds: workgroup b computes that of query b (the grid
-    // extends past the chunks to one workgroup per query), and every
-    // workgroup waits for its queries', so the whole grid must be resident at
-    // once (one 8-wave workgroup per CU).
+    // Sampling and thresholds in the scan: every workgroup samples the first
+    // in_spt tiles of its chunk (about as many tiles in all as the sampling
+    // pass would), workgroup b computes query b's threshold from all of
+    // them (the grid extends past the chunks to one workgroup per query), and
+    // every workgroup waits for those of its queries, so the whole grid must
+    // be resident at once (one 8-wave workgroup per CU).  Two units per
+    // chunk and query, at least 2k of them (unless sampling is forced).
     P.tau_in_scan = P.lean && P.s8 && !(flags & CVS_FLAG_TAU_LAUNCH) && P.groups == 1 &&
-                    std::max<int64_t>(P.chunks, nq) <= cus && P.s8_units <= 2 * 256 && d <= 512 && k <= 256;
+                    std::max<int64_t>(P.chunks, nq) <= cus && 2 * P.chunks <= 2 * 256 &&
+                    (P.chunks >= k || (flags & CVS_FLAG_FORCE_PREPASS)) && d <= 512 && k <= 256;
+    if (P.tau_in_scan) {
+      P.in_spt = std::max<int64_t>(1, std::min<int64_t>(P.tpc, ceil_div(P.s8_tiles, P.chunks)));
+      P.in_units = 2 * P.chunks;
+    }
   }
   const int64_t nqq = std::max<int64_t>(nq, 1);
   const int64_t lists = nqq * P.nlists;
@@ -960,10 +972,10 @@ int make_q8_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int flags, int cus
   off = align_up(off + lists * 4, 256);
   P.off_tau = off;
   off = align_up(off + nqq * 4, 256);
-  P.off_tauw = off;
-  if (P.tau_in_scan) off = align_up(off + nqq * 8, 256);
+  P.off_tauw = off;  // threshold words, then unit words (zeroed together)
+  if (P.tau_in_scan) off = align_up(off + nqq * (1 + P.in_units) * 8, 256);
   P.off_umax = off;
-  if (P.s8) {
+  if (P.s8 && !P.tau_in_scan) {
     off = align_up(off + nqq * P.s8_units * 4, 256);
     P.off_uarg = off;
     off = align_up(off + nqq * P.s8_units * 4, 256);
@@ -1036,7 +1048,8 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
   hipError_t e;
 
   if (!fp16_sample) {  // otherwise the threshold select quantises the queries on the way
-    Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm, qf};
+    // (and, for sampling in the scan, clears its threshold and unit words)
+    Q8QueryArgs qa{qh, nq, (int)d, (int)P.dq, qq, qm, qf, tauw, P.tau_in_scan ? nq * (1 + P.in_units) : 0};
     e = launch_q8_queries(qa, s);
     if (e != hipSuccess) return hip_fail(e, "query quantisation launch");
   }
@@ -1074,6 +1087,9 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     e = launch_select(5, ta, (int)nq, s);
     if (e != hipSuccess) return hip_fail(e, "threshold select launch");
     mark(2);
+  } else if (P.tau_in_scan) {  // sampling and thresholds inside the int8 scan
+    mark(1);
+    mark(2);
   } else if (P.s8) {  // int8 sampling pass; the threshold from rescoring its best units' rows
     ScanArgs pa{};
     pa.q = reinterpret_cast<const _Float16*>(qq);  // int8 rows in 2-byte units
@@ -1098,12 +1114,11 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
     pa.qmeta = qm;
     pa.bmeta = bmeta;
     pa.gamma = gamma;
-    pa.tauw = P.tau_in_scan ? tauw : nullptr;
     pa.perm = P.s8_agg ? perm : nullptr;  // units' rows as corpus rows (mapped in the pass's tail)
     e = launch_scan(P.cfg, kMaxQ8, pa, (int)(P.groups * P.s8_nsample), s);
     if (e != hipSuccess) return hip_fail(e, "int8 sample pass launch");
     mark(1);
-    if (!P.tau_in_scan) {  // (otherwise the int8 scan computes the thresholds itself)
+    {
       SelectArgs ta{};
       ta.lv = umax;
       ta.li = pa.uarg;
@@ -1231,13 +1246,13 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       a.tau = nullptr;
       a.tauw = tauw;
       a.tau_out = tau;
-      a.su_max = umax;
-      a.su_arg = reinterpret_cast<const int*>(ws + P.off_uarg);
-      a.su_units = (int)P.s8_units;
+      a.su_w = tauw + nq;
+      a.su_units = (int)P.in_units;
+      a.spt = (int)P.in_spt;
       a.qh = qh;
       a.xh = xh;
       a.dh = (int)d;
-      a.perm = P.s8_agg ? nullptr : perm;
+      a.perm = perm;  // units hold companion rows
     }
     const bool lean = P.lean && q8scan384_fits(a);
     if (P.tau_in_scan && !lean) return fail(CVS_ERR_INVALID, "internal: in-scan thresholds without the 384-byte int8 scan");

@@ -68,16 +68,17 @@ struct ScanArgs {
   const signed char* qf;  // the int8 queries in fragment order (q8_frag_offset): what the MFMAs load
   const float4* bmeta;  // [ceil(n/64)] (s_b, max |f_r|_2 up, max |x_r|_2 up, 0) per 64-row block
   float gamma;          // relative slack for fp32 rounding of the scores: (3d + 8) * 2^-24
-  // Thresholds computed inside the int8 scan (cvs_tau_group.h): when tauw is
-  // not null, the kMaxQ8 sampling pass zeroes tauw[0..nq) and the int8 scan
-  // (tau null) takes each query's threshold from the sampling units
-  // su_max / su_arg [nq, su_units] by exact rescoring against the fp16 query
-  // rows qh and corpus xh (dh halfs per row; perm: companion -> corpus row,
-  // null when su_arg holds corpus rows), also stored to tau_out[q].
+  // Sampling and thresholds inside the lean int8 scan (cvs_tau_group.h): when
+  // tauw is not null (tau null), each scanning workgroup first samples the
+  // first spt tiles of its chunk into su_w [nq, su_units] (one unit word per
+  // (query, row half), su_units = 2 * nchunks), then computes a threshold
+  // per query from those units by exact rescoring against the fp16 query
+  // rows qh and corpus xh (dh halfs per row; perm: companion -> corpus row),
+  // publishes it in tauw[q] and tau_out[q], and scans.  tauw and su_w are
+  // zeroed by the query quantisation that runs before the scan.
   unsigned long long* tauw;
   float* tau_out;
-  const float* su_max;
-  const int* su_arg;
+  unsigned long long* su_w;
   int su_units;
   const _Float16* qh;
   const _Float16* xh;
@@ -199,6 +200,8 @@ struct Q8QueryArgs {
   signed char* qq;     // [nq, dq]
   float4* qmeta;       // [nq]
   signed char* qf;     // when not null: the same bytes in fragment order (q8_frag_offset), 32 * ceil(nq / 32) * dq bytes
+  unsigned long long* zero;  // words [0, nzero) set to 0 (the lean int8 scan's unit and threshold words)
+  int64_t nzero;
 };
 
 // Scan configurations: MFMA shape ms (16 or 32), queries per wave 16*... = ms*qb,

@@ -159,8 +159,10 @@ __global__ __launch_bounds__(kBlock) void q8_xmax_kernel(const float4* bmeta, in
   if (threadIdx.x == 0) *xmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// One wave per query row.
+// One wave per query row; the whole grid also clears a.zero[0, nzero).
 __global__ __launch_bounds__(kBlock) void q8_query_kernel(Q8QueryArgs a) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < a.nzero; i += (int64_t)gridDim.x * kBlock)
+    a.zero[i] = 0ull;
   const int64_t r = (int64_t)blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
   if (r >= a.nq) return;  // whole wave
   q8_query_row(a.q + r * a.d, a.d, a.dq, a.qq + r * a.dq, a.qmeta + r, threadIdx.x & 63, a.qf, r);
@@ -205,7 +207,8 @@ hipError_t launch_q8_build(const Q8BuildArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_q8_queries(const Q8QueryArgs& a, hipStream_t s) {
-  if (a.d < 8 || a.d % 8 != 0 || a.d > kQ8RowPer * kWave || a.dq < a.d || a.dq > kQ8RowPer * kWave || a.dq % 128 != 0)
+  if (a.d < 8 || a.d % 8 != 0 || a.d > kQ8RowPer * kWave || a.dq < a.d || a.dq > kQ8RowPer * kWave || a.dq % 128 != 0 ||
+      a.nzero < 0 || (a.nzero > 0 && a.zero == nullptr))
     return hipErrorInvalidValue;
   const int64_t per = kBlock / kWave;
   const int64_t grid = (a.nq + per - 1) / per;

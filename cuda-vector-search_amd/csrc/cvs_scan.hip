@@ -220,11 +220,6 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     t_end = t_begin + a.tpc < a.ntiles ? t_begin + a.tpc : a.ntiles;
   }
 
-  if constexpr (MODE == kMaxQ8) {  // the words of the thresholds the int8 scan computes: "not yet"
-    if (a.tauw != nullptr && tid == 0)
-      for (int i = blockIdx.x; i < a.nq; i += gridDim.x) a.tauw[i] = 0ull;
-  }
-
   const int d = a.d;
   const int nc = FULLW ? NCMAX : (d >> 6);
   const int64_t n = a.n;

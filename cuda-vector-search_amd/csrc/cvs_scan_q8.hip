@@ -21,7 +21,15 @@
 //    plus a constant 32-bit lane offset (no per-load vector address
 //    arithmetic); stages past the workgroup's own tiles are not loaded.
 //  * The tile's block meta comes through the scalar cache, loaded one tile
-//    ahead and consumed after the next top-of-tile wait.
+//    ahead and consumed after the next mid-tile wait.
+//  * Sampling and thresholds in the same launch (tauw not null): each
+//    workgroup first runs the chunk's first spt tiles through the same MFMAs
+//    keeping, per (query, row half), the largest approximate score A and its
+//    row; publishes these units; computes one query's threshold from every
+//    workgroup's units (cvs_tau_group.h) while its ring already holds the
+//    first scanned tiles; then scans the whole chunk.  One launch replaces
+//    the sampling pass, its threshold select and their two launch gaps, and
+//    the sampled tiles' MFMAs run at the scan's rate.
 //
 // Stage layout (as the generic kernel's whole-tile stages): row R of a tile at
 // R * 384 bytes, three 128-byte lines, slot s of a line holding 16-byte piece
@@ -102,19 +110,31 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     const int L = (w + kQ8Waves * j) * 8 + (lane >> 3);  // stage line of this lane's piece
     voff[j] = (uint32_t)(L * 128 + (((lane & 7) ^ piece_swz(L / 3)) << 4));
   }
-  int64_t it_t = t_begin;
+  // The workgroup's tile sequence.  With sampling in the scan (a.tauw not
+  // null): the first spt tiles of its chunk, sampled, then every tile of the
+  // chunk, scanned (the sampled ones again, now against the thresholds);
+  // otherwise the chunk's tiles, scanned.  Workgroups past the scan's chunks
+  // (the grid extends to one workgroup per query) only compute their query's
+  // threshold.
+  const bool fused = a.tauw != nullptr;
+  const bool tau_only = fused && (int)blockIdx.x >= a.groups * a.nchunks;
+  const int64_t ntl = (tau_only || t_end <= t_begin) ? 0 : t_end - t_begin;
+  const int spt = fused ? (int)(a.spt < ntl ? a.spt : ntl) : 0;
+  const int64_t npos = spt + ntl;
+  auto tile_at = [&](int64_t p) -> int64_t { return t_begin + (p < spt ? p : p - spt); };
+  int64_t it_p = 0;
   int it_buf = 0;
-  // Stages past this workgroup's tiles are not loaded (the tile loop's waits
-  // account for it): prefetching them would read another chunk's tiles, ~5%
-  // of the corpus again over a launch, and the final drain would wait for them.
+  // Positions past the sequence are not loaded (the tile loop's waits account
+  // for it): prefetching them would read another chunk's tiles, ~5% of the
+  // corpus again over a launch, and the final drain would wait for them.
   auto issue_next = [&]() {
-    if (it_t < t_end) {
-      const unsigned char* base = xq + it_t * kQ8Stage;
+    if (it_p < npos) {
+      const unsigned char* base = xq + tile_at(it_p) * kQ8Stage;
       const uint32_t lds = lds0 + (uint32_t)(it_buf * kQ8Stage + w * 1024);
 #pragma unroll
       for (int j = 0; j < kQ8Lpw; ++j) dma16_saddr(voff[j], base, lds + (uint32_t)(j * kQ8Waves * 1024));
     }
-    ++it_t;
+    ++it_p;
     it_buf = (it_buf + 1 == kQ8Nbuf) ? 0 : it_buf + 1;
   };
   // ---- this lane's two queries: fragments (AGPRs), thresholds, bound terms ----
@@ -135,54 +155,27 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
       qm[qb] = a.qmeta[qc];
     }
   };
+  // Query blockIdx.x's threshold (waves 0-3; waves 4-7 keep step with the
+  // group's barriers), in the staging area, which holds no entries then.
   static_assert(2 * sizeof(TauGroupShared) <= sizeof(st_ent), "threshold scratch in the staging area");
-  if (a.tauw == nullptr) {
-#pragma unroll
-    for (int i = 0; i < kQ8Nbuf - 1; ++i) issue_next();
-  } else {
-    // Thresholds computed here: waves 0-3 take query blockIdx.x (tau_group,
-    // in the staging area, free until the first tile) while waves 4-7 issue
-    // every prologue stage load, their own and those of waves w - 4, so that
-    // no stage load sits in the threshold waves' vmcnt queue ahead of the
-    // threshold's loads.  (Every wave drains its loads before the tile loop.)
-    // The grid may extend past the scan's chunks (one workgroup per query):
-    // those workgroups only compute their query's threshold.
-    const bool tau_only = (int)blockIdx.x >= a.groups * a.nchunks;  // no chunk: thresholds only
-    if (w >= 4 && !tau_only) {
-#pragma unroll
-      for (int i = 0; i < kQ8Nbuf - 1; ++i) {
-        if (t_begin + i >= t_end) break;  // (as issue_next: only this workgroup's tiles)
-        const unsigned char* base = xq + (t_begin + i) * kQ8Stage;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int ww = w - 4 + 4 * h;
-          const uint32_t lds = lds0 + (uint32_t)(i * kQ8Stage + ww * 1024);
-#pragma unroll
-          for (int j = 0; j < kQ8Lpw; ++j) {
-            const int L = (ww + kQ8Waves * j) * 8 + (lane >> 3);
-            const uint32_t vo = (uint32_t)(L * 128 + (((lane & 7) ^ piece_swz(L / 3)) << 4));
-            dma16_saddr(vo, base, lds + (uint32_t)(j * kQ8Waves * 1024));
-          }
-        }
-      }
-    }
-    it_t = t_begin + (kQ8Nbuf - 1);
-    it_buf = kQ8Nbuf - 1;
-    TauGroupShared* tg = reinterpret_cast<TauGroupShared*>(&st_ent[0][0]);
+  TauGroupShared* tg = reinterpret_cast<TauGroupShared*>(&st_ent[0][0]);
+  auto threshold = [&]() {
     const int qt = (w < 4 && (int)blockIdx.x < a.nq) ? (int)blockIdx.x : -1;
-    tau_group<2, 4, 4>(tg[w >> 2], tid & 255, qt, a.su_max, a.su_arg, a.su_units, a.k, a.qh, a.xh, n, a.dh, a.perm, a.tauw,
+    tau_group<2, 4, 4>(tg[w >> 2], tid & 255, qt, a.su_w, a.su_units, a.k, a.qh, a.xh, n, a.dh, a.perm, a.tauw,
                        a.tau_out);
-    if (tau_only) return;
+  };
+  if (tau_only) {
+    threshold();
+    return;
   }
-  // (After the thresholds: issued before them, by any of the waves, these
-  // loads queue ahead of the threshold's in the CU's memory pipeline and
-  // delay it by more than they gain.)
+#pragma unroll
+  for (int i = 0; i < kQ8Nbuf - 1; ++i) issue_next();
   load_queries();
 
   for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
     const int qi = grp * kQ8Bq + i;
     lcnt[i] = 0;
-    if (a.tauw == nullptr) thr_s[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
+    if (!fused) thr_s[i] = (qi >= a.nq) ? __builtin_inff() : (a.tau ? a.tau[qi] : -__builtin_inff());
   }
   int st_n = 0;  // wave-uniform count of staged entries
 
@@ -261,17 +254,40 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     const cfloat_p m = meta + 4 * (t_begin < t_last ? t_begin : t_last);
     bm_next = float4{m[0], m[1], m[2], m[3]};
   }
+  // sampling: this lane's largest approximate score A = cq * sum of its rows
+  // (per query block) and its companion row, over the sampled tiles
+  float umx[2] = {-__builtin_inff(), -__builtin_inff()};
+  int uag[2] = {0, 0};
+  // One unit per (query, row half): the better of the two lane groups' (the
+  // lower row on ties), published as (row + 1) << 32 | bits(A).
+  auto publish_units = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float ov = __shfl_xor(umx[qb], 32);
+      const int orow = __shfl_xor(uag[qb], 32);
+      if (ov > umx[qb] || (ov == umx[qb] && orow < uag[qb])) {
+        umx[qb] = ov;
+        uag[qb] = orow;
+      }
+      const int qi = grp * kQ8Bq + qgw * 64 + qb * 32 + col;
+      if (kg == 0 && qi < a.nq)
+        __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + 2 * chunk + half],
+                           ((unsigned long long)(uag[qb] + 1) << 32) | __float_as_uint(umx[qb]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
 
-#pragma unroll 1
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    const float4 bm = bm_next;
+  // One tile of the sequence: its block meta (loaded a tile ahead) and its
+  // MFMAs, which also read the next position's first fragments.
+  auto tile_mfma = [&](int64_t p, float4& bm, i32x16& acc0, i32x16& acc1) {
+    const int64_t t = tile_at(p);
+    bm = bm_next;
     {
-      const int64_t tn = t + 1 < t_last ? t + 1 : t_last;
-      const cfloat_p m = meta + 4 * tn;
+      const int64_t tn = p + 1 < npos ? tile_at(p + 1) : t;
+      const cfloat_p m = meta + 4 * (tn < t_last ? tn : t_last);
       bm_next = float4{m[0], m[1], m[2], m[3]};
     }
     const int nxt = (cur + 1 == kQ8Nbuf) ? 0 : cur + 1;
-    i32x16 acc0, acc1;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       acc0[e] = 0;
@@ -280,16 +296,16 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
 #pragma unroll
     for (int ks = 0; ks < kQ8Ks; ++ks) {
       if (ks == kQ8Ks - 2) {
-        // The fragments read from here on are stage t+1's (the current
+        // The fragments read from here on are position p+1's (the current
         // stage's were published by the previous tile's barrier, so the
-        // MFMAs above overlap the waves' arrival here).  Stage t+1 has landed
+        // MFMAs above overlap the waves' arrival here).  Stage p+1 has landed
         // for every wave, and every read of the buffer that issue_next()
-        // refills (stage t-1's) has retired.  Stage t+2's loads may still be
+        // refills (stage p-1's) has retired.  Stage p+2's loads may still be
         // in flight, when it exists: near the end there is nothing after
-        // stage t+1 to leave outstanding.  (Exact for a ring of 4: one stage,
-        // t+2, may be outstanding, and it exists exactly when t + 2 < t_end.)
+        // stage p+1 to leave outstanding.  (Exact for a ring of 4: one stage,
+        // p+2, may be outstanding, and it exists exactly when p + 2 < npos.)
         static_assert(kQ8Nbuf == 4, "the end-of-range wait counts assume a ring of 4 stages");
-        if (t + 2 < t_end)
+        if (p + 2 < npos)
           wait_vmcnt_lgkm0<(kQ8Nbuf - 3) * kQ8Lpw>();
         else
           wait_vmcnt_lgkm0<0>();
@@ -305,25 +321,16 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
       acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[ks % 3], qf[1][ks], acc1, 0, 0, 0);
     }
     cur = nxt;
-    if (t == t_begin && a.tauw != nullptr) {
-      // the thresholds computed in the prologue (this workgroup's and the
-      // others'), waited for while the first tile's MFMAs run
-      for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
-        const int qi = grp * kQ8Bq + i;
-        thr_s[i] = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) thr[qb] = thr_s[qgw * 64 + qb * 32 + col];
-    }
+  };
+  // acc{qb}[e] = int8 score of query 64 qgw + 32 qb + col, row rowb +
+  // acc_row(e); rows past n (only in the corpus's last tile) get INT_MIN.
+  auto tile_rows = [&](int64_t p, i32x16& acc0, i32x16& acc1) -> int64_t {
     pad_mfma_result<8>(acc1);
     asm volatile("" : "+v"(acc0));
     asm volatile("" : "+v"(acc1));
-
-    // ---- epilogue: acc{qb}[e] = int8 score of query 64 qgw + 32 qb + col,
-    //      row rowb + acc_row(e) ----
+    const int64_t t = tile_at(p);
     const int64_t rowb = t * kQ8Tile + 32 * half + 4 * kg;
-    if (t * kQ8Tile + kQ8Tile > n) {  // only the corpus's last tile has rows past n
+    if (t * kQ8Tile + kQ8Tile > n) {
       const int64_t left = n - rowb;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -333,6 +340,56 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
         }
       }
     }
+    return rowb;
+  };
+
+  // ---- sampled tiles: the lane's largest sum of each (its first row on ties) ----
+#pragma unroll 1
+  for (int64_t p = 0; p < spt; ++p) {
+    float4 bm;
+    i32x16 acc0, acc1;
+    tile_mfma(p, bm, acc0, acc1);
+    const int64_t rowb = tile_rows(p, acc0, acc1);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const i32x16& acc = qb ? acc1 : acc0;
+      int mi = acc[0], me = 0;
+#pragma unroll
+      for (int e = 1; e < 16; ++e)
+        if (acc[e] > mi) {
+          mi = acc[e];
+          me = e;
+        }
+      const float av = mi == INT_MIN ? -__builtin_inff() : (float)mi * (qm[qb].x * bm.x);
+      if (av > umx[qb]) {
+        umx[qb] = av;
+        uag[qb] = (int)rowb + acc_row(me);
+      }
+    }
+  }
+  if (fused) {
+    publish_units();
+    threshold();  // waits for every workgroup's units of query blockIdx.x
+  }
+
+  // ---- scanned tiles ----
+#pragma unroll 1
+  for (int64_t p = spt; p < npos; ++p) {
+    float4 bm;
+    i32x16 acc0, acc1;
+    tile_mfma(p, bm, acc0, acc1);
+    if (fused && p == spt) {
+      // the thresholds (this workgroup's and the others'), waited for while
+      // the first scanned tile's MFMAs run
+      for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
+        const int qi = grp * kQ8Bq + i;
+        thr_s[i] = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) thr[qb] = thr_s[qgw * 64 + qb * 32 + col];
+    }
+    const int64_t rowb = tile_rows(p, acc0, acc1);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const i32x16& acc = qb ? acc1 : acc0;
@@ -375,15 +432,17 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
 
 bool q8scan384_fits(const ScanArgs& a) {
   if (a.tauw != nullptr &&
-      (a.tau != nullptr || a.tau_out == nullptr || a.su_max == nullptr || a.su_arg == nullptr || a.su_units < 1 || a.su_units > 2 * 256 ||
-       a.qh == nullptr || a.xh == nullptr || a.dh < 8 || a.dh % 8 != 0 || a.dh > 8 * 16 * 4 ||
-       a.k < 1 || a.k > 256))
+      (a.tau != nullptr || a.tau_out == nullptr || a.su_w == nullptr || a.su_units != 2 * a.nchunks ||
+       a.su_units > 2 * 256 || a.spt < 1 || a.qh == nullptr || a.xh == nullptr || a.dh < 8 || a.dh % 8 != 0 ||
+       a.dh > 8 * 16 * 4 || a.k < 1 || a.k > 256 || a.groups != 1))
     return false;
   return a.d * 2 == kQ8Row && a.qf != nullptr && a.qmeta != nullptr && a.bmeta != nullptr && a.nlists == a.nchunks;
 }
 
 hipError_t launch_q8scan384(const ScanArgs& a, int grid, hipStream_t s) {
   if (!q8scan384_fits(a)) return hipErrorInvalidValue;
+  // with sampling in the scan, workgroup q computes query q's threshold
+  if (a.tauw != nullptr && (grid < a.nq || grid < a.nchunks)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(q8scan384_kernel, dim3(grid), dim3(kQ8Waves * kWave), 0, s, a);
   return hipGetLastError();
 }

@@ -1,4 +1,4 @@
-// The int8 pre-filter's threshold computed inside the int8 scan's prologue.
+// The int8 pre-filter's threshold computed inside the int8 scan.
 //
 // tau_rescore_kernel (cvs_select.hip) derives each query's threshold from the
 // int8 sampling pass in a launch of its own: a 256-bin histogram of the units'
@@ -8,18 +8,22 @@
 // rows, so tau is at most the k-th best score of the search.
 //
 // tau_group() is the same computation for one query by one group of 256
-// threads (4 waves) of a larger workgroup: waves 0-3 of the scan's workgroup b
-// take query b (the grid has at least one workgroup per query), so the
-// dependent launch and its ramp disappear and the work overlaps the scan's
-// first stage loads, which waves 4-7 issue.  The result is published
-// as one 64-bit word per query, (1 << 32) | bits(tau), with an agent-scope
-// atomic store; every workgroup of the scan then waits for the words of its
-// queries (agent-scope atomic loads, coherent across the XCDs' L2s).  Words of
-// 0 mean "not yet": the sampling pass, which runs before the scan on the same
-// stream, zeroes them.  A bounded wait: a word still 0 after kTauWaitTicks of
-// the 100 MHz constant clock (workgroups of the scan that were not resident
-// together, e.g. on a GPU shared with other work) gives tau = -inf for that
-// query, which keeps the search exact (every row a candidate; lists that fill
+// threads (4 waves) of a larger workgroup, on units the same launch publishes:
+// every workgroup of the int8 scan first samples a few tiles of its chunk and
+// stores one unit per (query, row half) as a 64-bit word ((row + 1) << 32 |
+// bits(A)), with an agent-scope atomic store; waves 0-3 of workgroup b then
+// take query b (the grid has at least one workgroup per query), waiting for
+// the words of its units (agent-scope atomic loads, coherent across the XCDs'
+// L2s).  The threshold is published the same way, one word per query,
+// (1 << 32) | bits(tau), and every workgroup waits for the words of its
+// queries before its first scanned tile.  Words of 0 mean "not yet": the
+// query quantisation, which runs before the scan on the same stream, zeroes
+// them.  Bounded waits: a unit still missing after kTauWaitTicks of the
+// 100 MHz constant clock (workgroups of the scan that were not resident
+// together, e.g. on a GPU shared with other work) is left out, which leaves
+// tau a lower bound of the k-th best score (it is the k-th best of real rows
+// either way); a threshold word still 0 gives tau = -inf for that query.
+// Both keep the search exact (every row a candidate at worst; lists that fill
 // are rescanned by the select), only slower.
 #pragma once
 
@@ -38,14 +42,14 @@ struct TauGroupShared {
 };
 
 // Query q (q < 0: none, the group only keeps step with the workgroup's
-// barriers) from its `units` sampled units umax/uarg[q * units ..] (A and the
-// companion row), the fp16 query row qh + q * d and corpus xh (rows of d
-// halfs, n of them), perm (companion row -> corpus row).  gt = thread in the
-// group, 0..255; the group's first thread is a multiple of 64.  Every thread
-// of the workgroup calls it (it holds workgroup barriers); requires
-// units <= U * 256, k <= 256, d <= 8 * 16 * RL.
+// barriers) from the unit words uw[q * units ..] (A and the companion row
+// + 1), the fp16 query row qh + q * d and corpus xh (rows of d halfs, n of
+// them), perm (companion row -> corpus row).  gt = thread in the group,
+// 0..255; the group's first thread is a multiple of 64.  Every thread of the
+// workgroup calls it (it holds workgroup barriers); requires units <= U * 256,
+// k <= 256, d <= 8 * 16 * RL.
 template <int U, int RL, int RU>
-__device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, const float* umax, const int* uarg, int units,
+__device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, const unsigned long long* uw, int units,
                                           int k, const _Float16* qh, const _Float16* xh, int64_t n, int d,
                                           const int* perm, unsigned long long* tauw, float* tau_out) {
   const int gl = gt & 63, gw = gt >> 6;
@@ -58,14 +62,36 @@ __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, cons
     row[u] = 0;
   }
   if (q >= 0) {
-    const float* src = umax + (int64_t)q * units;
-    const int* rsrc = uarg + (int64_t)q * units;
+    const unsigned long long* src = uw + (int64_t)q * units;
+    unsigned long long v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {  // unconditional clamped loads: they issue together
       const int i = u * 256 + gt;
-      const int ic = i < units ? i : units - 1;
-      av[u] = src[ic];
-      row[u] = rsrc[ic];
+      v[u] = __hip_atomic_load(&src[i < units ? i : units - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the units of workgroups still sampling: wait (bounded) for their words
+    auto missing = [&]() {
+      bool m = false;
+#pragma unroll
+      for (int u = 0; u < U; ++u) m |= u * 256 + gt < units && (v[u] >> 32) == 0;
+      return m;
+    };
+    if (__any(missing())) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      do {
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int i = u * 256 + gt;
+          if (i < units && (v[u] >> 32) == 0)
+            v[u] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } while (__any(missing()) && __builtin_amdgcn_s_memrealtime() - t0 <= kTauWaitTicks);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      av[u] = __uint_as_float((unsigned)v[u]);
+      row[u] = (int)(v[u] >> 32) - 1;  // -1: missing
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {  // a unit counts when it has a row (A > -inf, row < n)

@@ -962,13 +962,15 @@ def test_q8_forced_sampling_with_few_units(eng, nq, n, d, k):
                                            (256, 120000, 100, False), (300, 200000, 10, False), (256, 9000, 250, True),
                                            (137, 5000, 40, True)])
 def test_q8_thresholds_in_the_scan_match_the_threshold_launch(eng, nq, n, k, forced):
-    """The 384-byte int8 scan computes each query's threshold in its prologue
-    (one query per 4 waves of a workgroup, published to the others through
-    64-bit words): bitwise the same results as the separate threshold launch
-    (FLAG_TAU_LAUNCH), and the fused path's.  Covers one and two query groups,
-    the batches whose candidates are rescored by a kernel of their own (fewer
-    than 160 queries: it reads the thresholds the scan stored), and forced
-    sampling over corpora with fewer sampled rows than k (threshold -inf)."""
+    """The 384-byte int8 scan samples the first tiles of each chunk and
+    computes each query's threshold itself (one query per 4 waves of a
+    workgroup; units and thresholds published to the other workgroups through
+    64-bit words): bitwise the same results as the sampling pass with its
+    separate threshold launch (FLAG_TAU_LAUNCH), and the fused path's.  Covers
+    one and two query groups, the batches whose candidates are rescored by a
+    kernel of their own (fewer than 160 queries: it reads the thresholds the
+    scan stored), and forced sampling over corpora with fewer sampled rows
+    than k (threshold -inf)."""
     say(f"q8 thresholds in the scan nq={nq} n={n} k={k} forced={forced}")
     x, q = make(n, 384, nq, seed=n + nq + k)
     qd = q.cuda().contiguous()
