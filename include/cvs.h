@@ -49,7 +49,8 @@ extern "C" {
 #define CVS_FLAG_FORCE_PREPASS 2 /* run the pre-pass whenever it is well defined */
 #define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
 #define CVS_FLAG_IDS_INT64 8     /* out_i is int64 (the dtype Index.search returns, index.py:126) */
-#define CVS_FLAG_TAU_LAUNCH 16   /* int8 pre-filter: thresholds in a launch of their own, not in the scan */
+#define CVS_FLAG_TAU_LAUNCH 16   /* int8 pre-filter: a sampling pass and a threshold launch of their own,
+                                    not the 384-byte int8 scan's own sampling and thresholds */
 #define CVS_FLAG_REGISTER_TOPK 32 /* fp16 fused path: a running top-k per lane in registers instead of the
                                      sampled threshold (batches 2..32, widths <= 384, k <= 16) */
 
@@ -204,7 +205,9 @@ int cvs_prep_rows(const void* src, void* dst, int64_t n, int64_t d, int64_t src_
  *   sampling pass), with the companion of x as xq.  plan_out[0] is the int8
  *   scan's query block, plan_out[1] its corpus chunks.
  * cvs_q8_topk_marked: as cvs_fused_topk_marked (events around: query
- *   quantisation + sampling pass, threshold select, int8 scan, rescore select).
+ *   quantisation + sampling pass, threshold select, int8 scan, rescore select;
+ *   where the int8 scan samples and takes the thresholds itself, the first
+ *   span is the quantisation alone and the second is empty).
  */
 int cvs_q8_corpus_bytes(int64_t n, int64_t d, int64_t* bytes);
 int cvs_q8_build(const void* x, int64_t n, int64_t d, void* xq, int64_t xq_bytes, int device, void* stream);
