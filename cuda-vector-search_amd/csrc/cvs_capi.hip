@@ -1247,6 +1247,7 @@ int run_q8(const void* q, const void* x, const void* xq, int64_t xq_bytes, int64
       a.tauw = tauw;
       a.tau_out = tau;
       a.su_w = tauw + nq;
+      a.no_wait = (flags & CVS_FLAG_TAU_NOWAIT) ? 1 : 0;
       a.su_units = (int)P.in_units;
       a.spt = (int)P.in_spt;
       a.qh = qh;

@@ -83,6 +83,7 @@ struct ScanArgs {
   const _Float16* qh;
   const _Float16* xh;
   int dh;
+  int no_wait;  // tests only (CVS_FLAG_TAU_NOWAIT): the waits above give up at once
   const int* perm;
 };
 

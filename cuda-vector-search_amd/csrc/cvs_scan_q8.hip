@@ -117,6 +117,9 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
   // (the grid extends to one workgroup per query) only compute their query's
   // threshold.
   const bool fused = a.tauw != nullptr;
+  // bound of each cross-workgroup wait (100 MHz ticks); 0 only in tests: every
+  // wait not satisfied at once gives up, which exercises the exact fallbacks
+  const uint64_t wait_ticks = a.no_wait ? 0 : kTauWaitTicks;
   const bool tau_only = fused && (int)blockIdx.x >= a.groups * a.nchunks;
   const int64_t ntl = (tau_only || t_end <= t_begin) ? 0 : t_end - t_begin;
   const int spt = fused ? (int)(a.spt < ntl ? a.spt : ntl) : 0;
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
   auto threshold = [&]() {
     const int qt = (w < 4 && (int)blockIdx.x < a.nq) ? (int)blockIdx.x : -1;
     tau_group<2, 4, 4>(tg[w >> 2], tid & 255, qt, a.su_w, a.su_units, a.k, a.qh, a.xh, n, a.dh, a.perm, a.tauw,
-                       a.tau_out);
+                       a.tau_out, wait_ticks);
   };
   if (tau_only) {
     threshold();
@@ -383,7 +386,7 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
       // the first scanned tile's MFMAs run
       for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
         const int qi = grp * kQ8Bq + i;
-        thr_s[i] = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi);
+        thr_s[i] = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi, wait_ticks);
       }
       __syncthreads();
 #pragma unroll

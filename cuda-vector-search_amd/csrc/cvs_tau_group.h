@@ -18,7 +18,7 @@
 // (1 << 32) | bits(tau), and every workgroup waits for the words of its
 // queries before its first scanned tile.  Words of 0 mean "not yet": the
 // query quantisation, which runs before the scan on the same stream, zeroes
-// them.  Bounded waits: a unit still missing after kTauWaitTicks of the
+// them.  Bounded waits: a unit still missing after `ticks` (kTauWaitTicks) of the
 // 100 MHz constant clock (workgroups of the scan that were not resident
 // together, e.g. on a GPU shared with other work) is left out, which leaves
 // tau a lower bound of the k-th best score (it is the k-th best of real rows
@@ -51,7 +51,7 @@ struct TauGroupShared {
 template <int U, int RL, int RU>
 __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, const unsigned long long* uw, int units,
                                           int k, const _Float16* qh, const _Float16* xh, int64_t n, int d,
-                                          const int* perm, unsigned long long* tauw, float* tau_out) {
+                                          const int* perm, unsigned long long* tauw, float* tau_out, uint64_t ticks) {
   const int gl = gt & 63, gw = gt >> 6;
   float av[U];
   int row[U];
@@ -86,7 +86,7 @@ __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, cons
           if (i < units && (v[u] >> 32) == 0)
             v[u] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-      } while (__any(missing()) && __builtin_amdgcn_s_memrealtime() - t0 <= kTauWaitTicks);
+      } while (__any(missing()) && __builtin_amdgcn_s_memrealtime() - t0 <= ticks);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -234,13 +234,13 @@ __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, cons
 }
 
 // The published threshold of query q: waits (bounded) for its word.
-__device__ __forceinline__ float tau_wait(const unsigned long long* tauw, int q) {
+__device__ __forceinline__ float tau_wait(const unsigned long long* tauw, int q, uint64_t ticks) {
   unsigned long long v = __hip_atomic_load(&tauw[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if ((v >> 32) == 0) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (((v = __hip_atomic_load(&tauw[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) == 0) {
       __builtin_amdgcn_s_sleep(2);
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kTauWaitTicks) return -__builtin_inff();
+      if (__builtin_amdgcn_s_memrealtime() - t0 > ticks) return -__builtin_inff();
     }
   }
   return __uint_as_float((unsigned)v);

@@ -53,6 +53,8 @@ extern "C" {
                                     not the 384-byte int8 scan's own sampling and thresholds */
 #define CVS_FLAG_REGISTER_TOPK 32 /* fp16 fused path: a running top-k per lane in registers instead of the
                                      sampled threshold (batches 2..32, widths <= 384, k <= 16) */
+#define CVS_FLAG_TAU_NOWAIT 64   /* tests only: the int8 scan's cross-workgroup waits give up at once
+                                    (the exact fallback of a GPU shared with other work, made certain) */
 
 /* Library version (CVS_VERSION). */
 int cvs_version(void);

@@ -88,6 +88,7 @@ def test_python_flags_match_header():
     assert _ext.FLAG_IDS_INT64 == int(d["CVS_FLAG_IDS_INT64"])
     assert _ext.FLAG_TAU_LAUNCH == int(d["CVS_FLAG_TAU_LAUNCH"])
     assert _ext.FLAG_REGISTER_TOPK == int(d["CVS_FLAG_REGISTER_TOPK"])
+    assert _ext.FLAG_TAU_NOWAIT == int(d["CVS_FLAG_TAU_NOWAIT"])
     m = re.search(r"#define\s+CVS_NOALLOC_SCRATCH_BYTES\s+\((\d+)ll << (\d+)\)", HEADER.read_text())
     assert m and _ext.NOALLOC_SCRATCH_BYTES == int(m[1]) << int(m[2])
 

@@ -990,6 +990,28 @@ def test_q8_thresholds_in_the_scan_match_the_threshold_launch(eng, nq, n, k, for
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,k", [(150000, 10), (120000, 100)])
+def test_q8_in_scan_waits_that_give_up_stay_exact(eng, n, k):
+    """The 384-byte int8 scan's workgroups wait for each other's unit and
+    threshold words with a bounded wait (a GPU shared with other work may not
+    hold them all at once).  CVS_FLAG_TAU_NOWAIT makes every wait that is not
+    satisfied at once give up: units left out, thresholds -inf, lists that
+    overflow and are rescanned by the select.  The results stay bitwise those
+    of the default search."""
+    say(f"q8 in-scan waits that give up n={n} k={k}")
+    x, q = make(n, 384, 256, seed=n + k + 5)
+    qd = q.cuda().contiguous()
+    xd = x.cuda().contiguous()
+    xq = eng.q8_build(xd)
+    v8, i8, _ = eng.q8_topk(qd, xd, xq, k)
+    vn, i_n, _ = eng.q8_topk(qd, xd, xq, k, flags=_ext.FLAG_TAU_NOWAIT)
+    torch.cuda.synchronize()
+    assert torch.equal(v8, vn) and torch.equal(i8, i_n)
+    sub = slice(0, 8)
+    oracle.check_exact(q[sub].numpy(), x.numpy(), k, vn[sub].cpu().numpy(), i_n[sub].cpu().numpy().astype(np.int64))
+
+
+@pytest.mark.gpu
 def test_q8_zero_queries_and_rows(eng):
     """All-zero queries (scale 0) and all-zero corpus blocks: every score is 0 and
     ties order by id."""
