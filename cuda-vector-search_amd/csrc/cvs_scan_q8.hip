@@ -13,7 +13,8 @@
 //    Each wave reads only its 32 rows of a tile from LDS and feeds each A
 //    fragment to two MFMAs (its two 32-query blocks): half the LDS fragment
 //    reads of 8 waves x 32 queries over all 64 rows.  Query fragments stay in
-//    AGPRs (2 x 12 x 16 bytes per lane).
+//    AGPRs (2 x 12 x 16 bytes per lane), loaded from the quantisation's
+//    fragment-ordered copy (1 KiB of contiguous memory per wave and k-step).
 //  * A tile is one 24 KB stage (64 rows x 384 bytes) and one 64-row block of
 //    the companion (one block-meta entry).  The companion is padded to whole
 //    64-row blocks, so no DMA load needs a bounds clamp: each of a wave's 3
