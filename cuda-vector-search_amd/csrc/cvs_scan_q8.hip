@@ -216,12 +216,17 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
       const int cnt = __popc(todo);
       const int pos = cnt ? atomicAdd(&lcnt[ql], cnt) : 0;
       const int room = a.cap - pos;
+      // The passing rows in ascending order, one per lane and round (rarely
+      // more than one per lane): bound and row from the entry's own sum in LDS.
       int put = 0;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if (((todo >> e) & 1u) && put < room) {
-          a.lv[lbase + pos + put] = ev[e];
-          a.li[lbase + pos + put] = rbase + acc_row(e);
+      while (__any(todo != 0u)) {
+        if (todo != 0u) {
+          const int e = __builtin_ctz(todo);
+          todo &= todo - 1u;
+          if (put < room) {
+            a.lv[lbase + pos + put] = fmaf((float)ent[e], cq, slack);
+            a.li[lbase + pos + put] = rbase + acc_row(e);
+          }
           ++put;
         }
       }
