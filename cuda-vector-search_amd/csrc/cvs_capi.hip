@@ -175,11 +175,16 @@ struct Plan {
   bool prepass = false;
   bool tau_in_scan = false;  // one sampling maximum per workgroup, thresholds found by the scan
   bool topk = false;         // CVS_FLAG_REGISTER_TOPK: running top-k in registers, no pre-pass
+  // sampling and thresholds inside the scan (mode kAppendIn) instead of the
+  // pre-pass and its threshold select: su_units units per query, the grid's
+  // sin_grid workgroups are the chunks and then the threshold workgroups
+  bool sin = false;
+  int64_t su_units = 0, sin_grid = 0;
   int64_t nsample = 0, spt = 1, units = 0;
   int agg = 0;
   int upb = 8;  // gemv sampling units per block
   // workspace
-  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, ws_bytes = 0;
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_tauw = 0, ws_bytes = 0;
 };
 
 // sample_div: the sampling pre-pass scores about 1/sample_div of the tiles (the
@@ -287,6 +292,34 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
         P.agg = 2;
         P.units = P.nsample;
       }
+      // Sampling inside the scan (d = 384, one query group): every scanning
+      // workgroup's first tile is its sample, one unit per query and row split
+      // (per lane group without row splits), and ceil(nq / waves) more workgroups take
+      // the thresholds from them, one query per wave.  Every workgroup waits
+      // for others, so the whole grid must fit the GPU at once (one per CU);
+      // at least 2k units per query.  Replaces the pre-pass, its threshold
+      // select and their launches (small corpora: all latency).
+      // Fewer chunks make room for the threshold workgroups when that costs at
+      // most one more tile per workgroup (an automatic chunk count only).
+      const int64_t nw = scan_waves(P.cfg.qs);
+      const int64_t twg = ceil_div(nq, nw);
+      int64_t c2 = P.chunks, tpc2 = P.tpc;
+      if (chunks == 0 && c2 + twg > cus && cus > twg) {
+        tpc2 = ceil_div(P.ntiles, cus - twg);
+        c2 = ceil_div(P.ntiles, tpc2);
+      }
+      const int64_t su = c2 * (P.cfg.rs() > 1 ? P.cfg.rs() : 64 / P.cfg.ms);  // (lane groups: one kernel, MS = 32)
+      if (allow_tau_in_scan && P.groups == 1 && scan_in_available(P.cfg, d) &&
+          !(flags & (CVS_FLAG_TAU_LAUNCH | CVS_FLAG_FORCE_PREPASS)) && c2 + twg <= cus && tpc2 <= P.tpc + 1 &&
+          su >= 2 * k && su <= 64 * (nw == 8 ? 8 : 32)) {
+        P.sin = true;
+        P.tau_in_scan = false;
+        P.chunks = c2;
+        P.tpc = tpc2;
+        P.nlists = c2 * P.cfg.rs();
+        P.su_units = su;
+        P.sin_grid = c2 + twg;
+      }
     }
   }
   if (flags & CVS_FLAG_REGISTER_TOPK) {
@@ -295,6 +328,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
     P.topk = true;
     P.prepass = false;
     P.tau_in_scan = false;
+    P.sin = false;
   }
   if (P.cap > kMaxCap) return fail(CVS_ERR_INVALID, "internal: list capacity %lld too large", (long long)P.cap);
   const int64_t lists = std::max<int64_t>(nq, 1) * P.nlists;
@@ -308,7 +342,9 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
   P.off_tau = off;
   off = align_up(off + std::max<int64_t>(nq, 1) * 4, 256);
   P.off_umax = off;
-  if (P.prepass) off = align_up(off + std::max<int64_t>(nq, 1) * P.units * 4, 256);
+  if (P.prepass && !P.sin) off = align_up(off + std::max<int64_t>(nq, 1) * P.units * 4, 256);
+  P.off_tauw = off;  // kAppendIn: threshold words, then unit words (cleared before the scan)
+  if (P.sin) off = align_up(off + std::max<int64_t>(nq, 1) * (1 + P.su_units) * 8, 256);
   P.ws_bytes = off;
   *p = P;
   return CVS_OK;
@@ -448,7 +484,18 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
     a.xcd_pair = P.xcd_pair;
     a.k = (int)k;
     a.cap = (int)P.cap;
-    if (P.prepass) {
+    if (P.sin) {  // sampling and thresholds inside the scan: clear their words first
+      unsigned long long* tauw = reinterpret_cast<unsigned long long*>(ws + P.off_tauw);
+      e = launch_zero_words(tauw, nq * (1 + P.su_units), s);
+      if (e != hipSuccess) return hip_fail(e, "word clear launch");
+      a.tauw = tauw;
+      a.tau_out = tau;
+      a.su_w = tauw + nq;
+      a.su_units = (int)P.su_units;
+      a.no_wait = (flags & CVS_FLAG_TAU_NOWAIT) ? 1 : 0;
+      mark(1);
+      mark(2);
+    } else if (P.prepass) {
       ScanArgs pa = a;
       pa.umax = umax;
       pa.nsample = (int)P.nsample;
@@ -484,7 +531,8 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
     a.lcount = cnt;
     a.nlists = (int)P.nlists;
     e = P.topk ? launch_scan_topk(P.cfg, a, (int)(P.groups * P.chunks), s)
-               : launch_scan(P.cfg, kAppend, a, (int)(P.groups * P.chunks), s);
+        : P.sin ? launch_scan_in(P.cfg, a, (int)P.sin_grid, s)
+                : launch_scan(P.cfg, kAppend, a, (int)(P.groups * P.chunks), s);
     if (e != hipSuccess) return hip_fail(e, "scan launch");
     mark(3);
   }

@@ -18,6 +18,9 @@ enum ScanMode : int {
                   // A = s_q s_b sum(q~ x~) over disjoint row sets, and its row
   kTopK = 6,      // no threshold: each lane keeps the k <= 16 best of its own scores of
                   // each query in registers (a running top-k) and appends them at the end
+  kAppendIn = 7,  // kAppend with its own sampling: each workgroup publishes the maxima of
+                  // its first tile as sampling units, threshold workgroups take each
+                  // query's threshold from them, and every workgroup filters with it
 };
 
 // One tile of corpus rows is scored against a group of queries by one
@@ -76,6 +79,11 @@ struct ScanArgs {
   // rows qh and corpus xh (dh halfs per row; perm: companion -> corpus row),
   // publishes it in tauw[q] and tau_out[q], and scans.  tauw and su_w are
   // zeroed by the query quantisation that runs before the scan.
+  // The fp16 scan in mode kAppendIn uses tauw, tau_out (may be null), su_w and
+  // su_units (= nchunks * row splits, or nchunks * lane groups without row
+  // splits: the maxima of each workgroup's first tile, (1 << 32) |
+  // float_order(max)) the same way, with the thresholds taken by the grid's
+  // extra workgroups; launch_zero_words clears them first.
   unsigned long long* tauw;
   float* tau_out;
   unsigned long long* su_w;
@@ -228,6 +236,14 @@ hipError_t launch_scan(const ScanCfg& cfg, int mode, const ScanArgs& a, int grid
 // Mode kTopK: instantiated for cfg {32, 1, 1, 1, 24} only (batches <= 32, width <= 384).
 bool scan_topk_available(const ScanCfg& cfg, int64_t d, int64_t k);
 hipError_t launch_scan_topk(const ScanCfg& cfg, const ScanArgs& a, int grid, hipStream_t s);
+// Mode kAppendIn: instantiated for full-width (d = 384) configs {32, 1, 1, 1, 24},
+// {32, 1, 2, 1, 24}, {32, 4, 1, 2, 24} and {32, 8, 1, 2, 24}, one query group.  The grid
+// is nchunks scanning workgroups and then ceil(nq / scan_waves(qs)) threshold workgroups
+// (one query per wave), all resident together.
+bool scan_in_available(const ScanCfg& cfg, int64_t d);
+hipError_t launch_scan_in(const ScanCfg& cfg, const ScanArgs& a, int grid, hipStream_t s);
+// Sets n 64-bit words to zero (the words the in-scan sampling waits on).
+hipError_t launch_zero_words(unsigned long long* p, int64_t n, hipStream_t s);
 // int8 scan of 384-byte rows at 256 queries per workgroup (cfg {32, 8, 1, 2, 12}):
 // the same lists as launch_scan(cfg, kAppendQ8, ...), from a leaner kernel.
 bool q8scan384_fits(const ScanArgs& a);

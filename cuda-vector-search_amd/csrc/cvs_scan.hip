@@ -39,10 +39,105 @@
 #include "cvs_common.h"
 #include "cvs_kernels.h"
 #include "cvs_q8_row.h"
+#include "cvs_tau_group.h"
 
 namespace cvs {
 
 namespace {
+
+// Wave-wide reductions (every lane active): the 8-lane DPP reductions, the
+// other half of each 16-lane row by row_mirror, then the four rows' lanes 0
+// through readlane (no LDS round trip).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max8_u32(v);
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min8_u32(v);
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  return min(min((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+             min((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v = sum8_i32(v);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
+// Mode kAppendIn, threshold workgroups: query q's threshold by one wave from
+// its su_units sampling units (words (1 << 32) | float_order(exact maximum) of
+// disjoint row sets; 0 = not yet published), at most 64 * UPL of them.  The
+// k-th largest unit key, found by the threshold select's bit search stopped
+// above the 12 low bits: a lower bound of the k-th largest unit, hence of the
+// query's k-th best score (k distinct rows score at least that much), at most
+// 2^-11 of the score below the unit.  Units still missing after `ticks` of the
+// 100 MHz clock are left out (fewer units: a lower threshold, still exact);
+// fewer than k present give -inf.  Published as (1 << 32) | bits(tau).
+template <int UPL>
+__device__ __forceinline__ void wave_unit_threshold(const ScanArgs& a, int q, int lane, uint64_t ticks) {
+  constexpr int kThrLowBits = 12;
+  const int U = a.su_units;
+  const unsigned long long* src = a.su_w + (int64_t)q * U;
+  unsigned long long v[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {  // unconditional clamped loads: they issue together
+    const int i = lane + kWave * j;
+    v[j] = __hip_atomic_load(&src[i < U ? i : U - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  auto missing = [&]() {
+    bool m = false;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) m |= lane + kWave * j < U && (v[j] >> 32) == 0;
+    return m;
+  };
+  if (__any(missing())) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    do {
+      __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) {
+        const int i = lane + kWave * j;
+        if (i < U && (v[j] >> 32) == 0) v[j] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } while (__any(missing()) && __builtin_amdgcn_s_memrealtime() - t0 <= ticks);
+  }
+  uint32_t key[UPL], hi = 0u, lo = ~0u;
+  int have = 0;
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const bool h = lane + kWave * j < U && (v[j] >> 32) != 0;
+    key[j] = h ? (uint32_t)v[j] : 0u;  // missing: below every unit
+    hi = max(hi, key[j]);
+    if (h) lo = min(lo, key[j]);
+    have += h ? 1 : 0;
+  }
+  hi = wave_max_u32(hi);
+  lo = wave_min_u32(lo);
+  uint32_t tk = 0u;  // order key 0: threshold -inf
+  if (wave_sum_i32(have) >= a.k) {
+    // tk starts at the bits every present key shares (at most the smallest of
+    // them, so at least k keys reach it) and keeps count(key >= tk) >= k
+    const uint32_t diff = hi ^ lo;
+    const int top = diff ? 31 - __builtin_clz(diff) : -1;
+    tk = (top < 0 ? hi : hi & ~((2u << top) - 1u)) & ~((1u << kThrLowBits) - 1u);
+    for (int bit = top; bit >= kThrLowBits; --bit) {
+      const uint32_t cand = tk | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) c += key[j] >= cand ? 1 : 0;
+      if (wave_sum_i32(c) >= a.k) tk = cand;
+    }
+  }
+  const float tv = order_threshold(tk);
+  if (lane == 0) {
+    if (a.tau_out != nullptr) a.tau_out[q] = tv;
+    __hip_atomic_store(&a.tauw[q], (1ull << 32) | (unsigned long long)__float_as_uint(tv), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 
 template <int MS>
 struct Mfma;
@@ -160,7 +255,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int G = kWave / MS;      // lane groups sharing a query column
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
   constexpr bool TOPK = (MODE == kTopK);
-  constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8);
+  constexpr bool SIN = (MODE == kAppendIn);  // fp16 append with its own sampling and thresholds
+  constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8 || SIN);
   static_assert(!TOPK || (QB == 1 && MS == 32), "running top-k: one 32-query block per wave");
   constexpr bool SMAX = (MODE == kMax || MODE == kMaxQ8);  // sample passes
   constexpr int STCAP = 64;          // staged entries per wave
@@ -178,7 +274,7 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   __shared__ float mred[MODE == kMax ? RS : 1][BQ];    // kMax, agg 2: maxima of the row splits
   __shared__ __attribute__((aligned(16))) float st_val[APP ? NW : 1][APP ? STCAP * EST : 1];  // staged entries
   __shared__ int st_meta[APP ? NW : 1][APP ? 2 * STCAP : 1];  // (query, first row) per entry
-  __shared__ uint64_t sortbuf[MODE == kAppend ? NW * kMaxCap : 1];  // compaction scratch (int8 lists never compact)
+  __shared__ uint64_t sortbuf[(MODE == kAppend || SIN) ? NW * kMaxCap : 1];  // compaction scratch (int8 lists never compact)
   // kStore*: each wave's [QW queries][RW rows] score tile, written out one query
   // row at a time by consecutive lanes (coalesced); rows padded by 4 elements.
   constexpr bool STORE = (MODE == kStoreF32 || MODE == kStoreF16);
@@ -190,6 +286,24 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   const int w = tid >> 6;
   const int qs = w % QS;
   const int rs = w / QS;
+  // kAppendIn: bound of each cross-workgroup wait (100 MHz ticks; 0 only in
+  // tests, where every wait not satisfied at once gives up), and the grid's
+  // workgroups past the scan's chunks: each wave takes one query's threshold.
+  const uint64_t wait_ticks = a.no_wait ? 0 : kTauWaitTicks;
+  if constexpr (SIN) {
+    if ((int)blockIdx.x >= a.groups * a.nchunks) {
+      const int q = ((int)blockIdx.x - a.groups * a.nchunks) * NW + w;
+      if (q < a.nq) {  // (8-wave kernels: at most 512 units, so that the registers suffice)
+        if (NW == 8 || a.su_units <= kWave * 8)
+          wave_unit_threshold<8>(a, q, lane, wait_ticks);
+        else if (a.su_units <= kWave * 16)
+          wave_unit_threshold<16>(a, q, lane, wait_ticks);
+        else
+          wave_unit_threshold<32>(a, q, lane, wait_ticks);
+      }
+      return;
+    }
+  }
   const int col = lane % MS;  // query column of this lane / A-fragment row
   const int kg = lane / MS;   // k-group of this lane (0..G-1)
 
@@ -777,6 +891,40 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
         st_n += __popcll(mk);
       }
     };
+    if constexpr (SIN) {
+      if (t == t_begin) {
+        // The first tile is this workgroup's sample: each lane's largest exact
+        // score of each query (rows past n left out) is one unit, published
+        // for the threshold workgroups; then the thresholds of the group's
+        // queries, waited for (bounded), replace the initial -inf before this
+        // tile's own candidates are staged.
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          float um = -__builtin_inff();
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int e = 0; e < M::NE; ++e)
+              if (!partial || rowb + rb * MS + M::row(e) < n) um = fmaxf(um, acc[qb][rb][e]);
+          // with row splits, one unit per (query, row split): the lane groups' larger
+          if constexpr (RS > 1) um = fmaxf(um, __shfl_xor(um, 32));
+          const int qi = qwave0 + qb * MS + col;
+          if (qi < a.nq && (RS == 1 || kg == 0))
+            __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + (RS > 1 ? chunk * RS + rs : chunk * G + kg)],
+                               (1ull << 32) | (unsigned long long)float_order(um), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        for (int i = tid; i < BQ; i += NT) {
+          const int qi = grp * BQ + i;
+          const float tv = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi, wait_ticks);
+#pragma unroll
+          for (int r = 0; r < RS; ++r) thr_s[r][i] = tv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
+      }
+    }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int qi = qwave0 + qb * MS + col;
@@ -1125,6 +1273,53 @@ bool scan_topk_available(const ScanCfg& c, int64_t d, int64_t k) {
 hipError_t launch_scan_topk(const ScanCfg& c, const ScanArgs& a, int grid, hipStream_t s) {
   if (!scan_topk_available(c, a.d, a.k) || a.cap < 2 * 16 || a.nlists != a.nchunks * c.rs()) return hipErrorInvalidValue;
   launch_mode<32, 1, 1, 1, 24, kTopK>(a.d == 24 * 16, a, grid, s);
+  return hipGetLastError();
+}
+
+// Mode kAppendIn: the full-width d = 384 configurations, one query group.
+#define CVS_SCAN_IN_CONFIGS(X) \
+  X(32, 1, 1, 1, 24)           \
+  X(32, 1, 2, 1, 24)           \
+  X(32, 4, 1, 2, 24)           \
+  X(32, 8, 1, 2, 24)
+
+bool scan_in_available(const ScanCfg& c, int64_t d) {
+#define CVS_HAS_IN(MS, QS, QB, RB, KS) \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) return d == KS * Mfma<MS>::KSZ;
+  CVS_SCAN_IN_CONFIGS(CVS_HAS_IN)
+#undef CVS_HAS_IN
+  return false;
+}
+
+hipError_t launch_scan_in(const ScanCfg& c, const ScanArgs& a, int grid, hipStream_t s) {
+  const int nw = scan_waves(c.qs);
+  if (!scan_in_available(c, a.d) || a.groups != 1 || a.tau != nullptr || a.umax_in != nullptr ||
+      a.tauw == nullptr || a.su_w == nullptr || a.su_units != a.nchunks * (c.rs() > 1 ? c.rs() : kWave / c.ms) ||
+      a.su_units > kWave * (nw == 8 ? 8 : 32) || a.nlists != a.nchunks * c.rs() || a.k < 1 || a.k > 256 ||
+      grid != a.nchunks + (a.nq + nw - 1) / nw)
+    return hipErrorInvalidValue;
+#define CVS_LAUNCH_IN(MS, QS, QB, RB, KS)                                     \
+  if (c.ms == MS && c.qs == QS && c.qb == QB && c.rb == RB && c.ksmax == KS) { \
+    hipLaunchKernelGGL((scan_kernel<MS, QS, QB, RB, KS, kAppendIn, true>), dim3(grid), dim3(nw * kWave), 0, s, a); \
+    return hipGetLastError();                                                  \
+  }
+  CVS_SCAN_IN_CONFIGS(CVS_LAUNCH_IN)
+#undef CVS_LAUNCH_IN
+  return hipErrorInvalidValue;
+}
+
+namespace {
+__global__ __launch_bounds__(kBlock) void zero_words_kernel(unsigned long long* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) p[i] = 0ull;
+}
+}  // namespace
+
+hipError_t launch_zero_words(unsigned long long* p, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (p == nullptr) return hipErrorInvalidValue;
+  const int64_t need = (n + kBlock - 1) / kBlock;
+  const int64_t blocks = need < 512 ? need : 512;
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, p, n);
   return hipGetLastError();
 }
 

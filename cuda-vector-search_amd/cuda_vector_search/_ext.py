@@ -44,9 +44,9 @@ FLAG_NO_PREPASS = 1
 FLAG_FORCE_PREPASS = 2
 FLAG_NO_GEMV = 4
 FLAG_IDS_INT64 = 8  # ids as int64 (Index.search's dtype) instead of the reference's int32
-FLAG_TAU_LAUNCH = 16  # int8 pre-filter: the thresholds in a launch of their own instead of in the scan
+FLAG_TAU_LAUNCH = 16  # the sampling pass and thresholds in launches of their own instead of in the scan
 FLAG_REGISTER_TOPK = 32  # fp16 path: a running top-k per lane in registers instead of the sampled threshold
-FLAG_TAU_NOWAIT = 64  # tests only: the int8 scan's cross-workgroup waits give up at once (exact fallback)
+FLAG_TAU_NOWAIT = 64  # tests only: the scans' cross-workgroup waits give up at once (exact fallback)
 NOALLOC_SCRATCH_BYTES = 96 << 20  # CVS_NOALLOC_SCRATCH_BYTES: scratch of cvs_fused_topk_noalloc per GPU
 
 

@@ -49,12 +49,14 @@ extern "C" {
 #define CVS_FLAG_FORCE_PREPASS 2 /* run the pre-pass whenever it is well defined */
 #define CVS_FLAG_NO_GEMV 4       /* batch 1 uses the MFMA scan instead of the GEMV path */
 #define CVS_FLAG_IDS_INT64 8     /* out_i is int64 (the dtype Index.search returns, index.py:126) */
-#define CVS_FLAG_TAU_LAUNCH 16   /* int8 pre-filter: a sampling pass and a threshold launch of their own,
-                                    not the 384-byte int8 scan's own sampling and thresholds */
+#define CVS_FLAG_TAU_LAUNCH 16   /* a sampling pass and a threshold launch of their own, not the scan's
+                                    own sampling and thresholds (the 384-byte int8 scan; the fp16 scan
+                                    at width 384 with one query group on a grid that fits the GPU) */
 #define CVS_FLAG_REGISTER_TOPK 32 /* fp16 fused path: a running top-k per lane in registers instead of the
                                      sampled threshold (batches 2..32, widths <= 384, k <= 16) */
-#define CVS_FLAG_TAU_NOWAIT 64   /* tests only: the int8 scan's cross-workgroup waits give up at once
-                                    (the exact fallback of a GPU shared with other work, made certain) */
+#define CVS_FLAG_TAU_NOWAIT 64   /* tests only: the scans' cross-workgroup waits for sampling units and
+                                    thresholds give up at once (the exact fallback of a GPU shared with
+                                    other work, made certain) */
 
 /* Library version (CVS_VERSION). */
 int cvs_version(void);

@@ -273,6 +273,51 @@ def test_prepass_does_not_change_results(eng, flags, n, d, b, k):
     np.testing.assert_array_equal(i, i0)
 
 
+# (32, 100000, 10): the 4-wave kernel, 196 scanning + 8 threshold workgroups;
+# (256, 100000, 100): the 8-wave kernel, 224 + 32, with near-duplicate rows;
+# (256, 60013, 50): fewer chunks (4 -> 5 tiles each) to fit the threshold
+# workgroups, a batch short of a multiple of the waves and a partial last tile;
+# (256, 6000, 10): units barely above 2k.
+@pytest.mark.parametrize("nq,n,k,ties", [(32, 100000, 10, False), (256, 100000, 100, True), (64, 60000, 10, False),
+                                         (128, 80000, 32, False), (250, 60013, 50, False), (17, 30011, 5, False),
+                                         (256, 6000, 10, False)])
+def test_fused_thresholds_in_the_scan_match_the_threshold_launch(eng, nq, n, k, ties):
+    """The fp16 scan at width 384 with one query group samples itself: every
+    workgroup publishes its first tile's per-lane maxima as units, the grid's
+    extra workgroups take each query's threshold from them (one query per
+    wave), and every workgroup filters with it.  Bitwise the results of the
+    separate sampling pass and threshold launch (FLAG_TAU_LAUNCH) and of no
+    sampling at all, and the oracle's."""
+    say(f"fp16 thresholds in the scan nq={nq} n={n} k={k} ties={ties}")
+    x, q = make(n, 384, nq, seed=n + nq + k)
+    if ties:
+        synthetic.inject_near_ties(x, seed=7)
+    v, i, plan = run_fused(eng, q, x, k)
+    vl, il, planl = run_fused(eng, q, x, k, flags=_ext.FLAG_TAU_LAUNCH)
+    vn, i_n, _ = run_fused(eng, q, x, k, flags=_ext.FLAG_NO_PREPASS)
+    assert plan[0] == planl[0]
+    np.testing.assert_array_equal(v, vl)
+    np.testing.assert_array_equal(i, il)
+    np.testing.assert_array_equal(v, vn)
+    np.testing.assert_array_equal(i, i_n)
+    sub = slice(0, 16)
+    oracle.check_exact(q[sub], x, k, v[sub], i[sub])
+
+
+@pytest.mark.parametrize("nq,n,k", [(32, 100000, 10), (256, 100000, 100)])
+def test_fused_in_scan_waits_that_give_up_stay_exact(eng, nq, n, k):
+    """The fp16 scan's waits for units and thresholds are bounded.
+    CVS_FLAG_TAU_NOWAIT makes every wait not satisfied at once give up (units
+    left out, thresholds -inf, lists compacted as they fill): the results stay
+    bitwise those of the default search."""
+    say(f"fp16 in-scan waits that give up nq={nq} n={n} k={k}")
+    x, q = make(n, 384, nq, seed=n + k + 9)
+    v, i, _ = run_fused(eng, q, x, k)
+    vn, i_n, _ = run_fused(eng, q, x, k, flags=_ext.FLAG_TAU_NOWAIT)
+    np.testing.assert_array_equal(v, vn)
+    np.testing.assert_array_equal(i, i_n)
+
+
 @pytest.mark.parametrize("n,d,b,k", [(100, 384, 5, 28), (65, 384, 3, 20), (65, 128, 3, 20), (100, 768, 5, 28),
                                      (130, 256, 40, 60), (70, 384, 200, 40)])
 def test_forced_prepass_with_fewer_finite_units_than_k(eng, n, d, b, k):
