@@ -293,8 +293,7 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
         P.units = P.nsample;
       }
       // Sampling inside the scan (d = 384, one query group): every scanning
-      // workgroup's first tile is its sample, one unit per query and row split
-      // (per lane group without row splits), and ceil(nq / waves) more workgroups take
+      // workgroup's first tile is its sample (units below), and ceil(nq / waves) more workgroups take
       // the thresholds from them, one query per wave.  Every workgroup waits
       // for others, so the whole grid must fit the GPU at once (one per CU);
       // at least 2k units per query.  Replaces the pre-pass, its threshold
@@ -308,7 +307,12 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
         tpc2 = ceil_div(P.ntiles, cus - twg);
         c2 = ceil_div(P.ntiles, tpc2);
       }
-      const int64_t su = c2 * (P.cfg.rs() > 1 ? P.cfg.rs() : 64 / P.cfg.ms);  // (lane groups: one kernel, MS = 32)
+      // one unit per (query, workgroup) when that leaves 8k of them (C1: 196
+      // units for k = 10 take the threshold waves' search 1.3 us less than 784
+      // per row split), else one per row split, per lane group without row
+      // splits (C5: 448 units for k = 100, 2.2 us faster than 224 per workgroup:
+      // the looser threshold costs more in candidates than the search saves)
+      const int64_t su = c2 >= 8 * k ? c2 : c2 * (P.cfg.rs() > 1 ? P.cfg.rs() : 64 / P.cfg.ms);
       if (allow_tau_in_scan && P.groups == 1 && scan_in_available(P.cfg, d) &&
           !(flags & (CVS_FLAG_TAU_LAUNCH | CVS_FLAG_FORCE_PREPASS)) && c2 + twg <= cus && tpc2 <= P.tpc + 1 &&
           su >= 2 * k && su <= 64 * (nw == 8 ? 8 : 32)) {

@@ -45,9 +45,9 @@ namespace cvs {
 
 namespace {
 
-// Wave-wide reductions (every lane active): the 8-lane DPP reductions, the
-// other half of each 16-lane row by row_mirror, then the four rows' lanes 0
-// through readlane (no LDS round trip).
+// Wave-wide maximum and minimum (every lane active): the 8-lane DPP
+// reductions, the other half of each 16-lane row by row_mirror, then the
+// four rows' lanes 0 through readlane (no LDS round trip).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max8_u32(v);
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
@@ -59,12 +59,6 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
   return min(min((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
              min((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
-}
-__device__ __forceinline__ int wave_sum_i32(int v) {
-  v = sum8_i32(v);
-  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
-  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-         __builtin_amdgcn_readlane(v, 48);
 }
 
 // Mode kAppendIn, threshold workgroups: query q's threshold by one wave from
@@ -104,6 +98,7 @@ __device__ __forceinline__ void wave_unit_threshold(const ScanArgs& a, int q, in
       }
     } while (__any(missing()) && __builtin_amdgcn_s_memrealtime() - t0 <= ticks);
   }
+  // (wave-wide counts as the popcounts of ballots: no cross-lane reduction)
   uint32_t key[UPL], hi = 0u, lo = ~0u;
   int have = 0;
 #pragma unroll
@@ -112,12 +107,12 @@ __device__ __forceinline__ void wave_unit_threshold(const ScanArgs& a, int q, in
     key[j] = h ? (uint32_t)v[j] : 0u;  // missing: below every unit
     hi = max(hi, key[j]);
     if (h) lo = min(lo, key[j]);
-    have += h ? 1 : 0;
+    have += __popcll(__ballot(h));
   }
   hi = wave_max_u32(hi);
   lo = wave_min_u32(lo);
   uint32_t tk = 0u;  // order key 0: threshold -inf
-  if (wave_sum_i32(have) >= a.k) {
+  if (have >= a.k) {
     // tk starts at the bits every present key shares (at most the smallest of
     // them, so at least k keys reach it) and keeps count(key >= tk) >= k
     const uint32_t diff = hi ^ lo;
@@ -127,8 +122,8 @@ __device__ __forceinline__ void wave_unit_threshold(const ScanArgs& a, int q, in
       const uint32_t cand = tk | (1u << bit);
       int c = 0;
 #pragma unroll
-      for (int j = 0; j < UPL; ++j) c += key[j] >= cand ? 1 : 0;
-      if (wave_sum_i32(c) >= a.k) tk = cand;
+      for (int j = 0; j < UPL; ++j) c += __popcll(__ballot(key[j] >= cand));
+      if (c >= a.k) tk = cand;
     }
   }
   const float tv = order_threshold(tk);
@@ -893,11 +888,20 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     };
     if constexpr (SIN) {
       if (t == t_begin) {
-        // The first tile is this workgroup's sample: each lane's largest exact
-        // score of each query (rows past n left out) is one unit, published
-        // for the threshold workgroups; then the thresholds of the group's
-        // queries, waited for (bounded), replace the initial -inf before this
-        // tile's own candidates are staged.
+        // The first tile is this workgroup's sample: the largest exact score
+        // of each query (rows past n left out) over the whole tile (one unit
+        // per workgroup, when there are 2k workgroups) or over each row
+        // split's rows (each lane group's without row splits) is a unit,
+        // published for the threshold workgroups; then the thresholds of the
+        // group's queries, waited for (bounded), replace the initial -inf
+        // before this tile's own candidates are staged.
+        const bool one = a.su_units == a.nchunks;
+        auto put_unit = [&](int qi, int u, float um) {
+          if (qi < a.nq)
+            __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + u],
+                               (1ull << 32) | (unsigned long long)float_order(um), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        };
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           float um = -__builtin_inff();
@@ -906,13 +910,23 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
 #pragma unroll
             for (int e = 0; e < M::NE; ++e)
               if (!partial || rowb + rb * MS + M::row(e) < n) um = fmaxf(um, acc[qb][rb][e]);
-          // with row splits, one unit per (query, row split): the lane groups' larger
-          if constexpr (RS > 1) um = fmaxf(um, __shfl_xor(um, 32));
-          const int qi = qwave0 + qb * MS + col;
-          if (qi < a.nq && (RS == 1 || kg == 0))
-            __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + (RS > 1 ? chunk * RS + rs : chunk * G + kg)],
-                               (1ull << 32) | (unsigned long long)float_order(um), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+          if (RS > 1 || one) um = fmaxf(um, __shfl_xor(um, 32));  // both lane groups
+          const int ql = qs * QW + qb * MS + col;
+          if (kg == 0 && one && RS > 1)
+            thr_s[rs][ql] = um;  // (the row splits' maxima meet below)
+          else if (RS == 1 && !one)
+            put_unit(grp * BQ + ql, chunk * G + kg, um);
+          else if (kg == 0)
+            put_unit(grp * BQ + ql, one ? chunk : chunk * RS + rs, um);
+        }
+        if (one && RS > 1) {
+          __syncthreads();
+          for (int i = tid; i < BQ; i += NT) {  // (each thread rewrites only its own entries below)
+            float um = thr_s[0][i];
+#pragma unroll
+            for (int r = 1; r < RS; ++r) um = fmaxf(um, thr_s[r][i]);
+            put_unit(grp * BQ + i, chunk, um);
+          }
         }
         for (int i = tid; i < BQ; i += NT) {
           const int qi = grp * BQ + i;
@@ -1294,7 +1308,8 @@ bool scan_in_available(const ScanCfg& c, int64_t d) {
 hipError_t launch_scan_in(const ScanCfg& c, const ScanArgs& a, int grid, hipStream_t s) {
   const int nw = scan_waves(c.qs);
   if (!scan_in_available(c, a.d) || a.groups != 1 || a.tau != nullptr || a.umax_in != nullptr ||
-      a.tauw == nullptr || a.su_w == nullptr || a.su_units != a.nchunks * (c.rs() > 1 ? c.rs() : kWave / c.ms) ||
+      a.tauw == nullptr || a.su_w == nullptr ||
+      (a.su_units != a.nchunks && a.su_units != a.nchunks * (c.rs() > 1 ? c.rs() : kWave / c.ms)) ||
       a.su_units > kWave * (nw == 8 ? 8 : 32) || a.nlists != a.nchunks * c.rs() || a.k < 1 || a.k > 256 ||
       grid != a.nchunks + (a.nq + nw - 1) / nw)
     return hipErrorInvalidValue;
