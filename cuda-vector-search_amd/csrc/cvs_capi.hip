@@ -184,7 +184,7 @@ struct Plan {
   int agg = 0;
   int upb = 8;  // gemv sampling units per block
   // workspace
-  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_tauw = 0, ws_bytes = 0;
+  int64_t off_lv = 0, off_li = 0, off_cnt = 0, off_tau = 0, off_umax = 0, off_tauw = 0, off_qfh = 0, ws_bytes = 0;
 };
 
 // sample_div: the sampling pre-pass scores about 1/sample_div of the tiles (the
@@ -349,6 +349,8 @@ int make_plan(int64_t nq, int64_t n, int64_t d, int64_t k, int64_t bq, int64_t c
   if (P.prepass && !P.sin) off = align_up(off + std::max<int64_t>(nq, 1) * P.units * 4, 256);
   P.off_tauw = off;  // kAppendIn: threshold words, then unit words (cleared before the scan)
   if (P.sin) off = align_up(off + std::max<int64_t>(nq, 1) * (1 + P.su_units) * 8, 256);
+  P.off_qfh = off;  // kAppendIn: the queries in fragment order (whole 32-query blocks)
+  if (P.sin) off = align_up(off + align_up(std::max<int64_t>(nq, 1), 32) * d * 2, 256);
   P.ws_bytes = off;
   *p = P;
   return CVS_OK;
@@ -488,10 +490,12 @@ int run_fused(const void* q, const void* x, int64_t nq, int64_t n, int64_t d, in
     a.xcd_pair = P.xcd_pair;
     a.k = (int)k;
     a.cap = (int)P.cap;
-    if (P.sin) {  // sampling and thresholds inside the scan: clear their words first
+    if (P.sin) {  // sampling and thresholds inside the scan: clear their words, copy the queries in fragment order
       unsigned long long* tauw = reinterpret_cast<unsigned long long*>(ws + P.off_tauw);
-      e = launch_zero_words(tauw, nq * (1 + P.su_units), s);
-      if (e != hipSuccess) return hip_fail(e, "word clear launch");
+      _Float16* qfh = reinterpret_cast<_Float16*>(ws + P.off_qfh);
+      e = launch_scan_in_prep(qh, (int)nq, (int)d, qfh, tauw, nq * (1 + P.su_units), s);
+      if (e != hipSuccess) return hip_fail(e, "scan prep launch");
+      a.qfh = qfh;
       a.tauw = tauw;
       a.tau_out = tau;
       a.su_w = tauw + nq;

@@ -83,7 +83,7 @@ struct ScanArgs {
   // su_units (= nchunks * row splits, or nchunks * lane groups without row
   // splits: the maxima of each workgroup's first tile, (1 << 32) |
   // float_order(max)) the same way, with the thresholds taken by the grid's
-  // extra workgroups; launch_zero_words clears them first.
+  // extra workgroups; launch_scan_in_prep clears them first, and writes qfh.
   unsigned long long* tauw;
   float* tau_out;
   unsigned long long* su_w;
@@ -93,6 +93,10 @@ struct ScanArgs {
   int dh;
   int no_wait;  // tests only (CVS_FLAG_TAU_NOWAIT): the waits above give up at once
   const int* perm;
+  // kAppendIn: the fp16 queries in fragment order (q8_frag_offset with d / 16
+  // k-steps of 16 halfs): the MFMAs' B operands, 1 KiB of contiguous memory per
+  // wave and k-step
+  const _Float16* qfh;
 };
 
 // Batch-1 GEMV: one query, rows split across waves, 8 lanes per row.
@@ -242,8 +246,11 @@ hipError_t launch_scan_topk(const ScanCfg& cfg, const ScanArgs& a, int grid, hip
 // (one query per wave), all resident together.
 bool scan_in_available(const ScanCfg& cfg, int64_t d);
 hipError_t launch_scan_in(const ScanCfg& cfg, const ScanArgs& a, int grid, hipStream_t s);
-// Sets n 64-bit words to zero (the words the in-scan sampling waits on).
-hipError_t launch_zero_words(unsigned long long* p, int64_t n, hipStream_t s);
+// Before a kAppendIn scan: sets nwords 64-bit words to zero (the unit and
+// threshold words it waits on) and writes the queries q [nq, d] (d = 384) in
+// fragment order into qfh (ceil(nq / 32) * 32 * d halfs).
+hipError_t launch_scan_in_prep(const _Float16* q, int nq, int d, _Float16* qfh, unsigned long long* words, int64_t nwords,
+                               hipStream_t s);
 // int8 scan of 384-byte rows at 256 queries per workgroup (cfg {32, 8, 1, 2, 12}):
 // the same lists as launch_scan(cfg, kAppendQ8, ...), from a leaner kernel.
 bool q8scan384_fits(const ScanArgs& a);

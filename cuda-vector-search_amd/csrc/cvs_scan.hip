@@ -434,6 +434,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       for (int ks = 0; ks < KSMAX; ++ks) {
         if constexpr (Q8)  // full-width int8 rows (KSMAX k-steps): the fragment-ordered copy, 1 KiB per load
           ld[qb][ks] = *(const half8*)(a.qf + q8_frag_offset(qi, ks, kg, KSMAX));
+        else if constexpr (SIN)  // the fp16 fragment-ordered copy, the same layout
+          ld[qb][ks] = *(const half8*)(reinterpret_cast<const char*>(a.qfh) + q8_frag_offset(qi, ks, kg, KSMAX));
         else
           ld[qb][ks] = *(const half8*)(a.q + (int64_t)qi * d + min(ks, ksl) * M::KSZ + kg * 8);
       }
@@ -1308,7 +1310,7 @@ bool scan_in_available(const ScanCfg& c, int64_t d) {
 hipError_t launch_scan_in(const ScanCfg& c, const ScanArgs& a, int grid, hipStream_t s) {
   const int nw = scan_waves(c.qs);
   if (!scan_in_available(c, a.d) || a.groups != 1 || a.tau != nullptr || a.umax_in != nullptr ||
-      a.tauw == nullptr || a.su_w == nullptr ||
+      a.tauw == nullptr || a.su_w == nullptr || a.qfh == nullptr ||
       (a.su_units != a.nchunks && a.su_units != a.nchunks * (c.rs() > 1 ? c.rs() : kWave / c.ms)) ||
       a.su_units > kWave * (nw == 8 ? 8 : 32) || a.nlists != a.nchunks * c.rs() || a.k < 1 || a.k > 256 ||
       grid != a.nchunks + (a.nq + nw - 1) / nw)
@@ -1324,17 +1326,38 @@ hipError_t launch_scan_in(const ScanCfg& c, const ScanArgs& a, int grid, hipStre
 }
 
 namespace {
-__global__ __launch_bounds__(kBlock) void zero_words_kernel(unsigned long long* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) p[i] = 0ull;
+// Thread i clears word i and copies 16-byte fragment piece i: piece o of the
+// copy is lane o % 64 of (32-query block, k-step) o / 64, i.e. 8 halfs of
+// query 32 * block + (lane % 32) at dims 16 * k-step + 8 * (lane / 32).
+__global__ __launch_bounds__(kBlock) void scan_in_prep_kernel(const _Float16* q, int nq, int d, _Float16* qfh,
+                                                              unsigned long long* words, int64_t nwords) {
+  const int ks_per_row = d / 16;
+  const int64_t npieces = (int64_t)((nq + 31) / 32) * ks_per_row * kWave;
+  const int64_t total = nwords > npieces ? nwords : npieces;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+    if (i < nwords) words[i] = 0ull;
+    if (i < npieces) {
+      const int lane = (int)(i % kWave);
+      const int64_t t = i / kWave;
+      const int ks = (int)(t % ks_per_row);
+      const int qi = (int)(t / ks_per_row) * 32 + (lane & 31);
+      half8 v = {};
+      if (qi < nq) v = *(const half8*)(q + (int64_t)qi * d + ks * 16 + (lane >> 5) * 8);
+      *(half8*)(qfh + i * 8) = v;
+    }
+  }
 }
 }  // namespace
 
-hipError_t launch_zero_words(unsigned long long* p, int64_t n, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  if (p == nullptr) return hipErrorInvalidValue;
-  const int64_t need = (n + kBlock - 1) / kBlock;
+hipError_t launch_scan_in_prep(const _Float16* q, int nq, int d, _Float16* qfh, unsigned long long* words, int64_t nwords,
+                               hipStream_t s) {
+  if (q == nullptr || qfh == nullptr || words == nullptr || nq < 1 || d < 16 || d % 16 != 0 || nwords < 0)
+    return hipErrorInvalidValue;
+  const int64_t npieces = (int64_t)((nq + 31) / 32) * (d / 16) * kWave;
+  const int64_t total = nwords > npieces ? nwords : npieces;
+  const int64_t need = (total + kBlock - 1) / kBlock;
   const int64_t blocks = need < 512 ? need : 512;
-  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, p, n);
+  hipLaunchKernelGGL(scan_in_prep_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, q, nq, d, qfh, words, nwords);
   return hipGetLastError();
 }
 
