@@ -251,6 +251,9 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
   constexpr int NV = RB * M::NE;     // scores per lane per query block per tile
   constexpr bool TOPK = (MODE == kTopK);
   constexpr bool SIN = (MODE == kAppendIn);  // fp16 append with its own sampling and thresholds
+  // kAppendIn, one wave per SIMD (registers to spare): tiles whose MFMAs run
+  // before the thresholds are known, their scores held in registers
+  constexpr int DEFER = (SIN && NW == 4) ? 3 : 1;
   constexpr bool APP = (MODE == kAppend || MODE == kAppendQ8 || SIN);
   static_assert(!TOPK || (QB == 1 && MS == 32), "running top-k: one 32-query block per wave");
   constexpr bool SMAX = (MODE == kMax || MODE == kMaxQ8);  // sample passes
@@ -758,8 +761,8 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     cur_buf = nxt;
   };
 
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    acc_t acc[QB][RB];
+  // One tile's MFMAs into acc; the stage pipeline advances by one tile.
+  auto tile_mfma = [&](acc_t (&acc)[QB][RB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
@@ -851,7 +854,66 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) asm volatile("" : "+v"(acc[qb][rb]));
+  };
 
+  // kAppendIn: the first tile is this workgroup's sample.  publish_units
+  // stores its units: the largest exact score of each query (rows past n left
+  // out) over the whole tile (one unit per workgroup, when there are 2k
+  // workgroups) or over each row split's rows (each lane group's without row
+  // splits), for the threshold workgroups.  wait_thresholds then reads the
+  // thresholds of the group's queries (bounded waits), which replace the
+  // initial -inf before any candidate is staged.
+  auto publish_units = [&](int64_t t, acc_t (&acc)[QB][RB]) {
+    const int64_t rowb = t * TR + rs * RW + 4 * kg;
+    const bool partial = (t * TR + TR > n);
+    const bool one = a.su_units == a.nchunks;
+    auto put_unit = [&](int qi, int u, float um) {
+      if (qi < a.nq)
+        __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + u],
+                           (1ull << 32) | (unsigned long long)float_order(um), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    };
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float um = -__builtin_inff();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < M::NE; ++e)
+          if (!partial || rowb + rb * MS + M::row(e) < n) um = fmaxf(um, acc[qb][rb][e]);
+      if (RS > 1 || one) um = fmaxf(um, __shfl_xor(um, 32));  // both lane groups
+      const int ql = qs * QW + qb * MS + col;
+      if (kg == 0 && one && RS > 1)
+        thr_s[rs][ql] = um;  // (the row splits' maxima meet below)
+      else if (RS == 1 && !one)
+        put_unit(grp * BQ + ql, chunk * G + kg, um);
+      else if (kg == 0)
+        put_unit(grp * BQ + ql, one ? chunk : chunk * RS + rs, um);
+    }
+    if (one && RS > 1) {
+      __syncthreads();
+      for (int i = tid; i < BQ; i += NT) {  // (each thread rewrites only its own entries below)
+        float um = thr_s[0][i];
+#pragma unroll
+        for (int r = 1; r < RS; ++r) um = fmaxf(um, thr_s[r][i]);
+        put_unit(grp * BQ + i, chunk, um);
+      }
+    }
+  };
+  auto wait_thresholds = [&]() {
+    for (int i = tid; i < BQ; i += NT) {
+      const int qi = grp * BQ + i;
+      const float tv = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi, wait_ticks);
+#pragma unroll
+      for (int r = 0; r < RS; ++r) thr_s[r][i] = tv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
+  };
+
+  // The epilogue of tile t from its scores acc.
+  auto tile_epilogue = [&](int64_t t, acc_t (&acc)[QB][RB]) {
     // ---- epilogue: acc[qb][rb][e] = score(query qwave0 + MS*qb + col,
     //                                        row rowb + MS*rb + M::row(e))
     const int64_t rowb = t * TR + rs * RW + 4 * kg;
@@ -888,57 +950,10 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
         st_n += __popcll(mk);
       }
     };
-    if constexpr (SIN) {
+    if constexpr (SIN && DEFER == 1) {
       if (t == t_begin) {
-        // The first tile is this workgroup's sample: the largest exact score
-        // of each query (rows past n left out) over the whole tile (one unit
-        // per workgroup, when there are 2k workgroups) or over each row
-        // split's rows (each lane group's without row splits) is a unit,
-        // published for the threshold workgroups; then the thresholds of the
-        // group's queries, waited for (bounded), replace the initial -inf
-        // before this tile's own candidates are staged.
-        const bool one = a.su_units == a.nchunks;
-        auto put_unit = [&](int qi, int u, float um) {
-          if (qi < a.nq)
-            __hip_atomic_store(&a.su_w[(int64_t)qi * a.su_units + u],
-                               (1ull << 32) | (unsigned long long)float_order(um), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        };
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          float um = -__builtin_inff();
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int e = 0; e < M::NE; ++e)
-              if (!partial || rowb + rb * MS + M::row(e) < n) um = fmaxf(um, acc[qb][rb][e]);
-          if (RS > 1 || one) um = fmaxf(um, __shfl_xor(um, 32));  // both lane groups
-          const int ql = qs * QW + qb * MS + col;
-          if (kg == 0 && one && RS > 1)
-            thr_s[rs][ql] = um;  // (the row splits' maxima meet below)
-          else if (RS == 1 && !one)
-            put_unit(grp * BQ + ql, chunk * G + kg, um);
-          else if (kg == 0)
-            put_unit(grp * BQ + ql, one ? chunk : chunk * RS + rs, um);
-        }
-        if (one && RS > 1) {
-          __syncthreads();
-          for (int i = tid; i < BQ; i += NT) {  // (each thread rewrites only its own entries below)
-            float um = thr_s[0][i];
-#pragma unroll
-            for (int r = 1; r < RS; ++r) um = fmaxf(um, thr_s[r][i]);
-            put_unit(grp * BQ + i, chunk, um);
-          }
-        }
-        for (int i = tid; i < BQ; i += NT) {
-          const int qi = grp * BQ + i;
-          const float tv = qi >= a.nq ? __builtin_inff() : tau_wait(a.tauw, qi, wait_ticks);
-#pragma unroll
-          for (int r = 0; r < RS; ++r) thr_s[r][i] = tv;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) thr[qb] = thr_s[rs][qs * QW + qb * MS + col];
+        publish_units(t, acc);
+        wait_thresholds();
       }
     }
 #pragma unroll
@@ -1110,6 +1125,33 @@ __global__ __launch_bounds__(scan_waves(QS) * kWave, 1) void scan_kernel(ScanArg
       }
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
+  };
+
+  int64_t t_first = t_begin;
+  if constexpr (SIN && DEFER > 1) {
+    // The first DEFER tiles' MFMAs run before the thresholds are known (the
+    // first tile's units published as soon as its scores are in), their
+    // scores held in registers; then their epilogues.  The MFMAs of tiles 2..
+    // DEFER fill the wait for the thresholds.
+    acc_t accd[DEFER][QB][RB];
+    const int64_t nd = t_end - t_begin < DEFER ? t_end - t_begin : DEFER;
+#pragma unroll
+    for (int dd = 0; dd < DEFER; ++dd) {
+      if (dd < nd) {
+        tile_mfma(accd[dd]);
+        if (dd == 0) publish_units(t_begin, accd[0]);
+      }
+    }
+    if (nd > 0) wait_thresholds();
+#pragma unroll
+    for (int dd = 0; dd < DEFER; ++dd)
+      if (dd < nd) tile_epilogue(t_begin + dd, accd[dd]);
+    t_first = t_begin + nd;
+  }
+  for (int64_t t = t_first; t < t_end; ++t) {
+    acc_t acc[QB][RB];
+    tile_mfma(acc);
+    tile_epilogue(t, acc);
   }
   if (APP && st_n > 0) flush();
   if constexpr (TOPK) {
