@@ -141,22 +141,36 @@ __device__ __forceinline__ void block_sort_desc(uint64_t* keys, int N) {
   }
 }
 
-// Descending sort of keys[0..nb) in place for nb <= kBlock: thread t counts the
-// keys above its own (keys are unique, so the counts are a permutation of
-// 0..nb-1) and moves its key to that slot.  Two barriers instead of the
-// bitonic network's log2(N)(log2(N)+1)/2; every lane reads the same key at a
-// time (an LDS broadcast).  Whole block.
+// Descending sort of keys[0..nb) in place for nb <= kBlock: each key's rank is
+// the number of keys above it (keys are unique, so the ranks are a permutation
+// of 0..nb-1), and the key moves to that slot.  G = min(8, kBlock / P) threads
+// (P = nb rounded up to a power of two) count for each key, thread t over the
+// t / P-th of G slices of the keys, so a short buffer still keeps every wave
+// busy; thread t < nb sums its key's G counts.  Two barriers instead of the
+// bitonic network's log2(N)(log2(N)+1)/2; every lane of a wave reads the same
+// key at a time (an LDS broadcast).  Whole block.
 __device__ __forceinline__ void block_rank_sort(uint64_t* keys, int nb) {
+  __shared__ int part[kBlock];
   const int tid = threadIdx.x;
+  int P = 1;
+  while (P < nb) P <<= 1;
+  const int G = min(8, kBlock / P);
+  const int i = tid & (P - 1), g = tid / P;
+  const int per = (nb + G - 1) / G;
+  const int j0 = min(nb, g * per), j1 = min(nb, j0 + per);
   uint64_t mine = 0;
   int rank = 0;
-  if (tid < nb) {
-    mine = keys[tid];
+  if (i < nb && g < G) {
+    mine = keys[i];
 #pragma unroll 8
-    for (int i = 0; i < nb; ++i) rank += keys[i] > mine ? 1 : 0;  // (reads in flight together)
+    for (int j = j0; j < j1; ++j) rank += keys[j] > mine ? 1 : 0;  // (reads in flight together)
   }
+  part[tid] = rank;
   __syncthreads();
-  if (tid < nb) keys[rank] = mine;
+  if (tid < nb) {  // (g == 0: mine is keys[tid])
+    for (int gg = 1; gg < G; ++gg) rank += part[gg * P + tid];
+    keys[rank] = mine;
+  }
   __syncthreads();
 }
 
@@ -315,6 +329,33 @@ __device__ __forceinline__ int list_of(const SH& S, int NL, int gi) {
   return lo;
 }
 
+// Smallest / largest of v over the wave (DPP within rows of 16 lanes, then the
+// four rows' results by readlane; every lane must be active): quad_perm
+// [1,0,3,2] and [2,3,0,1] combine each quad, row_half_mirror the two quads of a
+// half-row, row_mirror the two halves of a row.  fminf / fmaxf as the shuffle
+// reductions they replace (a NaN loses to any number).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_min_f32(float v) {
+  v = fminf(v, dpp_f32<0xB1>(v));
+  v = fminf(v, dpp_f32<0x4E>(v));
+  v = fminf(v, dpp_f32<0x141>(v));
+  v = fminf(v, dpp_f32<0x140>(v));
+  return fminf(fminf(lane_f32(v, 0), lane_f32(v, 16)), fminf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+
 // Smallest of keys[0..nb) (~0 when nb == 0).  Whole block; `red` is kWaves
 // words of LDS.
 __device__ __forceinline__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {
@@ -370,11 +411,13 @@ __device__ __forceinline__ void hist_cut_bin(const int (*hist)[256], int k, int*
 // Loose cut of the buffer's keys by score: a 256-bin histogram over the
 // scores' [min, max] picks the fewest top bins holding at least k keys, and
 // every key in them (m >= k keys, exactly those >= the returned key) is kept,
-// compacted to keys[0..m).  Seven barriers, where the exact radix cut needs
-// three or four per 8-bit digit.  Returns 0 and leaves the buffer alone when
-// m would exceed `limit` (many keys sharing a score).  Whole block; nb > k.
+// compacted to keys[0..m).  Seven barriers (five without want_min), where the
+// exact radix cut needs three or four per 8-bit digit.  Returns the smallest
+// kept key (0 without want_min), or 0 leaving the buffer alone when m would
+// exceed `limit` (many keys sharing a score).  Whole block; nb > k.
 template <class SH>
-__device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* red, int* m_out) {
+__device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int limit, uint64_t* red, int* m_out,
+                                                   bool want_min = true) {
   constexpr int PER = kBuf / kBlock;
   __shared__ float mm[2][kWaves];
   const int tid = threadIdx.x;
@@ -392,11 +435,8 @@ __device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int lim
       hi = fmaxf(hi, v);
     }
   }
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off));
-    hi = fmaxf(hi, __shfl_xor(hi, off));
-  }
+  lo = wave_min_f32(lo);
+  hi = wave_max_f32(hi);
   if (lane == 0) {
     mm[0][w] = lo;
     mm[1][w] = hi;
@@ -436,7 +476,7 @@ __device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int lim
   for (int j = 0; j < PER; ++j)
     if (j * kBlock + tid < nb && bin(r[j]) >= bstar) S.keys[atomicAdd(&S.ncut, 1)] = r[j];
   __syncthreads();
-  return block_min_key(S.keys, m, red);
+  return want_min ? block_min_key(S.keys, m, red) : 0ull;
 }
 
 // End of a batch of appends.  When the next batch might not fit, the buffer is
@@ -445,15 +485,17 @@ __device__ __forceinline__ uint64_t block_cut_hist(SH& S, int nb, int k, int lim
 // batch the buffer is cut to at most kBlock keys that hold its k best the same
 // way and sorted by rank, leaving the k best first.  Whole block.  Every thread
 // reads the count before any thread can append again, so all take the same
-// branch.
+// branch.  Returns true when keys[0..min(nbuf, k)) are sorted (descending).
 template <bool HIST = true, class SH>
-__device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
+__device__ __forceinline__ bool end_batch(SH& S, int k, bool last) {
   __shared__ uint64_t red[kWaves];
   __syncthreads();
   int nb = S.nbuf;
+  bool sorted = false;
   if (!HIST) {  // exact cuts only (the row top-k: large k, registers needed elsewhere)
     if (last && nb <= kBlock) {
       block_rank_sort(S.keys, nb);
+      sorted = true;
       if (threadIdx.x == 0 && nb > k) {
         S.nbuf = k;
         S.thr_key = S.keys[k - 1];
@@ -484,7 +526,7 @@ __device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
     uint64_t kth = 0ull;
     if (nb > kBlock) {  // down to at most kBlock keys holding the k best
       int m = 0;
-      block_cut_hist(S, nb, k, kBlock, red, &m);
+      block_cut_hist(S, nb, k, kBlock, red, &m, false);
       if (m > kBlock) {
         kth = block_keep_top(S, nb, k);
         m = k;
@@ -493,6 +535,7 @@ __device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
     }
     if (nb <= kBlock) {
       block_rank_sort(S.keys, nb);  // sorted: the k best first
+      sorted = true;
       if (threadIdx.x == 0) {
         S.nbuf = k;
         S.thr_key = S.keys[k - 1];
@@ -503,6 +546,7 @@ __device__ __forceinline__ void end_batch(SH& S, int k, bool last) {
     }
   }
   __syncthreads();
+  return sorted;
 }
 
 
@@ -544,6 +588,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   if (MODE == kSelTau && quant) q8_load_row(a.q + (int64_t)q * a.d, a.d, tid - kWave, qrow);
 
   const int total = list_prefix(S, a, q, false);
+  bool sorted = false;
   for (int base = 0; base < total; base += kBatch) {
     const uint64_t t = S.thr_key;
     // all of this thread's list lookups and loads first, then the appends: an
@@ -569,7 +614,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
       const uint64_t key = make_key(val[j], idv[j]);
       if (base + j * kBlock + tid < total && key > t) S.keys[atomicAdd(&S.nbuf, 1)] = key;
     }
-    end_batch(S, k, base + kBatch >= total);
+    sorted = end_batch(S, k, base + kBatch >= total);
   }
 
   const int nb = min(S.nbuf, k);
@@ -584,6 +629,8 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
       for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
       if (tid == 0) a.tau[q] = (nb >= k) ? key_score(m) : -__builtin_inff();
     }
+  } else if (sorted) {
+    write_keys(S.keys, a, q, nb);
   } else {
     write_topk(S, a, q, nb);
   }
@@ -817,11 +864,8 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
       if (lst[j] >= 0) cand((j0 + j) * kBlock + tid) = ok ? make_key(uv[j], idv[j]) : 0ull;
     }
   }
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off));
-    hi = fmaxf(hi, __shfl_xor(hi, off));
-  }
+  lo = wave_min_f32(lo);
+  hi = wave_max_f32(hi);
   if (lane == 0) {
     mm[0][w] = lo;
     mm[1][w] = hi;
@@ -943,11 +987,8 @@ __global__ __launch_bounds__(kBlock) void tau_rescore_kernel(SelectArgs a) {
     nrow = 0;
     nex = 0;
   }
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off));
-    hi = fmaxf(hi, __shfl_xor(hi, off));
-  }
+  lo = wave_min_f32(lo);
+  hi = wave_max_f32(hi);
   if (lane == 0) {
     mm[0][w] = lo;
     mm[1][w] = hi;
