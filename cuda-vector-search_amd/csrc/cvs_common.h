@@ -66,6 +66,21 @@ __device__ __forceinline__ uint32_t max8_u32(uint32_t v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: row_shr 1, 2, 4 and 8
+// within each row of 16 lanes (lanes shifted in from outside the row add 0),
+// then row_bcast:15 adds the last lane of rows 0 and 2 to rows 1 and 3, and
+// row_bcast:31 that of row 1 (the sum of rows 0-1 by then) to rows 2 and 3.
+// Every lane must be active.
+__device__ __forceinline__ int wave_incl_sum_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 __device__ __forceinline__ uint32_t min8_u32(uint32_t v) {
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));

@@ -80,12 +80,7 @@ __device__ __forceinline__ uint64_t block_keep_top(SH& S, int nb, int k) {
         s += c[j];
       }
       // exclusive prefix over lanes of s (descending bin order)
-      int incl = s;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int o = __shfl_up(incl, off);
-        if (lane >= off) incl += o;
-      }
+      int incl = wave_incl_sum_i32(s);
       int run = incl - s;  // keys in bins strictly above this lane's first bin
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -289,12 +284,7 @@ __device__ __forceinline__ int list_prefix(SH& S, const SelectArgs& a, int q, bo
       v[j] = S.part[4 * tid + j];
       s += v[j];
     }
-    int incl = s;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int o = __shfl_up(incl, off);
-      if (tid >= off) incl += o;
-    }
+    int incl = wave_incl_sum_i32(s);
     int run = incl - s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -387,12 +377,7 @@ __device__ __forceinline__ void hist_cut_bin(const int (*hist)[256], int k, int*
     c[j] = hist[0][b] + hist[1][b] + hist[2][b] + hist[3][b];
     sum += c[j];
   }
-  int incl = sum;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int o = __shfl_up(incl, off);
-    if (lane >= off) incl += o;
-  }
+  int incl = wave_incl_sum_i32(sum);
   int run = incl - sum;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -1231,12 +1216,7 @@ __global__ __launch_bounds__(kBlock) void rescore_kernel(SelectArgs a) {
     if (c > a.cap) c = 0;  // overflowed: left to the select
   }
   kept[tid] = 0;
-  int v = c;  // inclusive scan of the list counts
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int o = __shfl_up(v, off);
-    if (lane >= off) v += o;
-  }
+  int v = wave_incl_sum_i32(c);  // inclusive scan of the list counts
   if (lane == kWave - 1) wsum[tid / kWave] = v;
   __syncthreads();
   for (int i = 0; i < tid / kWave; ++i) v += wsum[i];

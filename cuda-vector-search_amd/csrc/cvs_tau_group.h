@@ -141,12 +141,7 @@ __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, cons
       c[j] = L.hist[0][b] + L.hist[1][b] + L.hist[2][b] + L.hist[3][b];
       sum += c[j];
     }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off);
-      if (gl >= off) incl += o;
-    }
+    int incl = wave_incl_sum_i32(sum);
     int run = incl - sum;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
