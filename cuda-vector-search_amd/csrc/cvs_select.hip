@@ -319,33 +319,6 @@ __device__ __forceinline__ int list_of(const SH& S, int NL, int gi) {
   return lo;
 }
 
-// Smallest / largest of v over the wave (DPP within rows of 16 lanes, then the
-// four rows' results by readlane; every lane must be active): quad_perm
-// [1,0,3,2] and [2,3,0,1] combine each quad, row_half_mirror the two quads of a
-// half-row, row_mirror the two halves of a row.  fminf / fmaxf as the shuffle
-// reductions they replace (a NaN loses to any number).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_f32(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-__device__ __forceinline__ float wave_min_f32(float v) {
-  v = fminf(v, dpp_f32<0xB1>(v));
-  v = fminf(v, dpp_f32<0x4E>(v));
-  v = fminf(v, dpp_f32<0x141>(v));
-  v = fminf(v, dpp_f32<0x140>(v));
-  return fminf(fminf(lane_f32(v, 0), lane_f32(v, 16)), fminf(lane_f32(v, 32), lane_f32(v, 48)));
-}
-__device__ __forceinline__ float wave_max_f32(float v) {
-  v = fmaxf(v, dpp_f32<0xB1>(v));
-  v = fmaxf(v, dpp_f32<0x4E>(v));
-  v = fmaxf(v, dpp_f32<0x141>(v));
-  v = fmaxf(v, dpp_f32<0x140>(v));
-  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
-}
-
 // Smallest of keys[0..nb) (~0 when nb == 0).  Whole block; `red` is kWaves
 // words of LDS.
 __device__ __forceinline__ uint64_t block_min_key(const uint64_t* keys, int nb, uint64_t* red) {

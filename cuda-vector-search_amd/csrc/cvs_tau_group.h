@@ -109,11 +109,8 @@ __device__ __forceinline__ void tau_group(TauGroupShared& L, int gt, int q, cons
     L.nrow = 0;
     L.nex = 0;
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off));
-    hi = fmaxf(hi, __shfl_xor(hi, off));
-  }
+  lo = wave_min_f32(lo);
+  hi = wave_max_f32(hi);
   if (gl == 0) {
     L.mm[0][gw] = lo;
     L.mm[1][gw] = hi;
