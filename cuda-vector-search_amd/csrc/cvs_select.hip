@@ -749,11 +749,17 @@ __device__ __forceinline__ void rescore_rows(uint64_t* out, int* cnt, const int*
   }
 }
 
+// The first rescoring pass takes at least this many rows (the top bins holding
+// max(k, kFirstPassMin) bounds): for small k its exact k-th best then sits
+// high enough that the second pass rarely has rows left, and the search saves
+// that pass's round trip of row loads.
+constexpr int kFirstPassMin = 32;
+
 // The int8 final stage in one pass over the candidates, when no list
 // overflowed and there are at most 2 * kBuf of them: every entry is read once
 // into LDS as a (U, corpus row) key (S.keys, then exb); the keys of the top
-// bins of a 256-bin histogram of U (m >= k of them, at most kBlock) are
-// rescored, and the k-th best of their exact keys, kappa, bounds the final
+// bins of a 256-bin histogram of U (m >= max(k, kFirstPassMin) of them when
+// there are that many, at most kBlock) are rescored, and the k-th best of their exact keys, kappa, bounds the final
 // k-th best key from below (they are real rows); then every other candidate
 // whose U reaches score(kappa) is rescored at once (a candidate below it has
 // S' <= U < score(kappa) and cannot enter).  The same rows' exact keys as the
@@ -848,7 +854,8 @@ __device__ __forceinline__ bool final_in_lds(SelShared& S, uint64_t* exb, uint64
     if (kk != 0ull) atomicAdd(&S.hist[w][bin(kk)], 1);
   }
   __syncthreads();
-  if (w == 0) hist_cut_bin(S.hist, k, &S.digit, &S.above);  // (bin 0, all keys, when fewer than k)
+  // (bin 0, all keys, when fewer than k1min)
+  if (w == 0) hist_cut_bin(S.hist, max(k, kFirstPassMin), &S.digit, &S.above);
   __syncthreads();
   const int bstar = S.digit;
   if (S.above > kBlock) return false;
