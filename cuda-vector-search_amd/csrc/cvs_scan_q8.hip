@@ -57,12 +57,14 @@ constexpr int kQ8Waves = 8;
 constexpr int kQ8Bq = 256;                  // queries per workgroup
 constexpr int kQ8Lpw = kQ8Stage / 1024 / kQ8Waves;  // DMA loads per wave per stage
 constexpr int kQ8Stcap = 64;                // staged entries per wave
+constexpr int kQ8LateKs = 4;                // k-step of the tile barrier of row half 1's waves
 // A staged entry is one lane's 16 int32 sums of one (query block, tile) and
 // (query in group, first row, cq, slack): 80 bytes, an odd count of 16-byte
 // units, so the ds_write_b128s of 16 consecutive entries hit distinct banks.
 constexpr int kQ8Est = 20;
 static_assert(kQ8Lpw * kQ8Waves * 1024 == kQ8Stage, "a stage is whole 1 KB loads, the same count per wave");
 static_assert(kQ8Ks % 3 == 0, "the 3-slot fragment ring needs the k-steps of a tile in multiples of 3");
+static_assert(kQ8LateKs < kQ8Ks - 2, "row half 1's tile barrier comes before its first read of the next stage");
 
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
@@ -287,7 +289,12 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
   };
 
   // One tile of the sequence: its block meta (loaded a tile ahead) and its
-  // MFMAs, which also read the next position's first fragments.
+  // MFMAs, which also read the next position's first fragments.  The waves of
+  // row half 0 take the tile's barrier two k-steps before its end, those of
+  // row half 1 kQ8LateKs k-steps into it: the two waves of a SIMD (one of each
+  // half: wave w and w + 4) then reach their epilogues half a tile apart, and
+  // each one's epilogue runs beside the other's MFMAs instead of both leaving
+  // the matrix core idle at once.  Every wave still takes one barrier per tile.
   auto tile_mfma = [&](int64_t p, float4& bm, i32x16& acc0, i32x16& acc1) {
     const int64_t t = tile_at(p);
     bm = bm_next;
@@ -304,12 +311,15 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     }
 #pragma unroll
     for (int ks = 0; ks < kQ8Ks; ++ks) {
-      if (ks == kQ8Ks - 2) {
-        // The fragments read from here on are position p+1's (the current
-        // stage's were published by the previous tile's barrier, so the
-        // MFMAs above overlap the waves' arrival here).  Stage p+1 has landed
-        // for every wave, and every read of the buffer that issue_next()
-        // refills (stage p-1's) has retired.  Stage p+2's loads may still be
+      if ((ks == kQ8Ks - 2 && half == 0) || (ks == kQ8LateKs && half == 1)) {
+        // The fragments read from k-step kQ8Ks - 2 on are position p+1's (the
+        // current stage's were published by the previous tile's barrier, so
+        // the MFMAs above overlap the waves' arrival here).  Stage p+1 has
+        // landed for every wave, and every read of the buffer that
+        // issue_next() refills (stage p-1's) has retired: row half 1's waves
+        // are kQ8LateKs k-steps into stage p, whose reads do not touch p-1's
+        // buffer, and the buffer refilled at the next barrier (stage p's) is
+        // read by no wave after its k-step kQ8Ks - 1 of this tile.  Stage p+2's loads may still be
         // in flight, when it exists: near the end there is nothing after
         // stage p+1 to leave outstanding.  (Exact for a ring of 4: one stage,
         // p+2, may be outstanding, and it exists exactly when p + 2 < npos.)
