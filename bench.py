@@ -5,7 +5,7 @@
 A step is one ``Index.search(queries, k)`` over one batch with the corpus and the
 queries already resident in HBM (the reference's methodology,
 bench/bench_gpu.py:105,124: an ``ip`` index over unit vectors, so cosine
-without per-call query normalisation).  The headline workload is BASELINE
+without per-call query normalisation).  The headline workload is benchmark
 config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
 ``configs_detail``.  One JSON line goes to stdout:
 

@@ -3,7 +3,7 @@
 Restates the reference's GPU tests (tests/test_search.py:47-169) against the
 oracle instead of torch, and adds: the committed golden vectors, the batch-1
 GEMV path, the sampling pre-pass on/off, list compaction under adversarial
-ordering, exact ties, the BASELINE configs at full size (every query at
+ordering, exact ties, the benchmark configs at full size (every query at
 C1, C3 and C5, 64 spread queries at C2 and C4, both exact paths), and an
 int8 companion kept current when the corpus changes.
 
@@ -485,7 +485,7 @@ def _spread_queries(b: int, want: int = 64) -> np.ndarray:
 
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
 def test_baseline_configs_full_size(eng, name):
-    """The five BASELINE configs at full size, through Index.search (auto: the
+    """The five benchmark configs at full size, through Index.search (auto: the
     int8 pre-filter at C2-C4, the fp16 scan at C1/C5) and method="fused":
     every query at C1, C3 and C5 (the near-tie config), 64 queries spread over
     every query group, wave and lane column at C2 and C4; ids and scores at the
