@@ -25,7 +25,7 @@ config C2 (1M x 384 corpus, batch 256, k=10); the other configs are reported in
 * configs_detail: one row per config with the same W warm-up and K timed calls:
   ms per batch, queries/s, per-stage device times, the dominant kernel's
   fraction of its roofline on its own bytes, and the end-to-end roofline of
-  BASELINE.md section 2 (achieved = max(F/P_fp16, B/BW) / t with F = 2 b n d,
+  the whole search (achieved = max(F/P_fp16, B/BW) / t with F = 2 b n d,
   B = 2 n d + 2 b d + 12 b k, both component fractions), plus that config's
   CPU baseline;
 * cpu_baseline: the reference's CPU search path (fp32 torch matmul + topk,
@@ -66,7 +66,7 @@ METRIC = "queries/sec at 1M×384 b256 k10; ms/batch + HBM GB/s at 4M×768 b1"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP16_PEAK = 2.5e15
 MFMA_INT8_PEAK = 5.0e15
-REF_T4_QPS_C2 = 13178.5  # reference fused kernel on a Tesla T4, C2
+REF_T4_QPS_C2 = 13178.5  # reference fused kernel on a Tesla T4 at C2 (results/t4.json:380-391, README.md:113)
 
 
 def log(*a):
@@ -84,7 +84,7 @@ def kernel_bytes_q8(n, dq, b):
 
 
 def end_to_end(n, d, b, k, ms, int8, dq):
-    """the whole search against max(F/P, B/BW) with
+    """The whole search against its roofline max(F/P, B/BW) with
     F = 2 b n d (fp16 MFMA peak) and B = 2 n d + 2 b d + 12 b k (the fp16
     corpus read once), whatever path ran; both component fractions."""
     f = 2.0 * b * n * d
@@ -476,7 +476,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(row["qps"] / REF_T4_QPS_C2, 3) if row["config"] == "C2" else None,
-        "vs_baseline_ref": "reference fused kernel on a Tesla T4 (BASELINE.md), not MI355X",
+        "vs_baseline_ref": "reference fused kernel on a Tesla T4 (results/t4.json:380-391), not MI355X",
         "dtype": ("int8 pre-filter (int32 accumulate, rigorous bound) + exact fp16 rescoring (fp32 accumulate)"
                   if row["path"] == "int8" else "fp16 in, fp32 accumulate"),
         "data": "synthetic: seeded N(0,1) rows, L2-normalised, stored fp16 (cuda_vector_search.synthetic)",
