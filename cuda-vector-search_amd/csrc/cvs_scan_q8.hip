@@ -174,8 +174,7 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     threshold();
     return;
   }
-#pragma unroll
-  for (int i = 0; i < kQ8Nbuf - 1; ++i) issue_next();
+  issue_next();  // stage 0 first; stages 1 and 2 once it and the queries are in
   load_queries();
 
   for (int i = tid; i < kQ8Bq; i += kQ8Waves * kWave) {
@@ -236,9 +235,13 @@ __global__ __launch_bounds__(kQ8Waves * kWave, 1) void q8scan384_kernel(ScanArgs
     st_n = 0;
   };
 
-  // Retire the query and threshold loads and the prologue stages before the
-  // loop (so the loop's waits count only stage loads), then start.
+  // Retire the query and threshold loads and stage 0 before the loop (so the
+  // loop's waits count only stage loads), then issue stages 1 and 2 and start:
+  // the launch's first burst of HBM reads is one stage instead of three (back-to-back
+  // C2 searches 1.2 us faster on average over five interleaved A/Bs).
   wait_vmcnt_lgkm0<0>();
+#pragma unroll
+  for (int i = 1; i < kQ8Nbuf - 1; ++i) issue_next();
   __builtin_amdgcn_s_barrier();
 
   // LDS offsets of this lane's A fragment pieces: k-step ks of row
